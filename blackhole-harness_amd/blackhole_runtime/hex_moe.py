@@ -1,0 +1,382 @@
+"""HEX fused MoE on MI355X: the operator API of runtime/blackhole_runtime/hex_moe.py over HIP
+kernels for gfx950 (libbh_hex.so, C ABI in include/bh_hex.h).
+
+Same names, arguments and errors as the reference module, so the `blackhole-hex` vLLM plugin
+(vllm_hex.py) and its callers use it unchanged:
+
+    HexTier(bits, experts, gate_proj, up_proj, down_proj).prepare(num_experts)
+    hex_moe(x, topk_weights, topk_ids, tiers, config=None, path="auto") -> [T, H] in x.dtype
+    hex_moe_fused / hex_moe_dequant / dequant_all / align / direct / plan / default_config
+
+Two ways through a layer, as in the reference (hex_moe.py:7-23):
+
+fused   the HIP kernels: slot plan (direct for a handful of slots, else the align kernel), then
+        per tier the gate/up kernel (SiLU fused) and the down kernel (top-k weight fused), then
+        the k-slot sum. No host synchronisation, so a hipGraph (torch.cuda.graph) captures it.
+dequant every expert decoded once by the dequant kernel into bf16/f16/f32 stacks, then one
+        matrix product per routed expert (rocBLAS through torch). It is taken for float32
+        activations (the fused kernels run the matrix cores in bf16/f16), for path="dequant", and
+        by path="auto" at or above BLACKHOLE_HEX_DEQUANT_MIN slots outside graph capture.
+
+Everything runs on the GPU; CPU tensors are refused (the reference's CPU route is its
+Triton interpreter, whose role the tests give to the numpy oracle).
+"""
+
+from __future__ import annotations
+
+import os
+from dataclasses import dataclass, field
+
+import torch
+
+from blackhole_runtime import _lib
+
+PARTS = ("idx", "block_scale", "expert_scale", "levels")
+PROJS = ("gate_proj", "up_proj", "down_proj")
+HEX_BLOCK = 32     # inputs per bit stream (blackhole/anatomy/hex.py:44)
+
+DIRECT_MAX = int(os.environ.get("BLACKHOLE_HEX_DIRECT_MAX", "32"))      # slots (hex_moe.py:260)
+DEQUANT_MIN = int(os.environ.get("BLACKHOLE_HEX_DEQUANT_MIN", "1024"))  # slots (hex_moe.py:261)
+
+
+def _n_in(p: dict, bits: int) -> int:
+    return p["idx"].shape[-1] // bits * HEX_BLOCK
+
+
+def _proj_struct(p: dict, bits: int) -> _lib.HexProj:
+    idx, bs = p["idx"], p["block_scale"]
+    n_in = _n_in(p, bits)
+    nblk = bs.shape[-1]
+    if nblk == 0 or n_in % nblk:
+        raise ValueError(f"block_scale width {nblk} does not divide the input width {n_in}")
+    return _lib.HexProj(idx.data_ptr(), bs.data_ptr(), p["expert_scale"].data_ptr(), p["levels"].data_ptr(),
+                        idx.stride(0), idx.stride(1), bs.stride(0), bs.stride(1), n_in // nblk)
+
+
+@dataclass
+class HexTier:
+    """One tier of a MoE layer: experts sharing one index width, stacked in the HEX layout
+    (hex_moe.py:174-198). Each projection dict holds idx uint32 [n, out, in/32*bits],
+    block_scale uint8 [n, out, in/B], expert_scale float32 [n], levels float32 [n, 2**bits]."""
+    bits: int
+    experts: torch.Tensor
+    gate_proj: dict
+    up_proj: dict
+    down_proj: dict
+    lookup: torch.Tensor | None = None
+    _structs: dict = field(default_factory=dict, repr=False, compare=False)
+    _experts_host: torch.Tensor | None = field(default=None, repr=False, compare=False)
+
+    def prepare(self, num_experts: int) -> "HexTier":
+        """Kernel-ready views (uint32 words as int32, float32 scales and levels, contiguous) and
+        the global -> tier-local expert map (-1 for experts of other tiers), as in the reference;
+        also the C structs the kernels take."""
+        if self.bits not in (3, 4):
+            raise ValueError(f"HEX tiers are 3- or 4-bit, got {self.bits}")
+        L = 1 << self.bits
+        for name in PROJS:
+            p = getattr(self, name)
+            if p["idx"].dtype == torch.uint32:
+                p["idx"] = p["idx"].view(torch.int32)
+            p["expert_scale"] = p["expert_scale"].float().reshape(-1).contiguous()
+            p["levels"] = p["levels"].float().contiguous()
+            for k in ("idx", "block_scale"):
+                p[k] = p[k].contiguous()
+            if p["levels"].shape[-1] != L:
+                raise ValueError(f"{name}: {p['levels'].shape[-1]} levels for a {self.bits}-bit tier")
+        dev = self.gate_proj["idx"].device
+        self._experts_host = self.experts.detach().to("cpu", torch.int64)
+        if self._experts_host.numel() and (int(self._experts_host.min()) < 0
+                                           or int(self._experts_host.max()) >= num_experts):
+            raise ValueError(f"tier expert ids must be in 0..{num_experts - 1}")
+        lk = torch.full((num_experts,), -1, dtype=torch.int32, device=dev)
+        lk[self.experts.to(dev).long()] = torch.arange(len(self.experts), dtype=torch.int32, device=dev)
+        self.lookup = lk
+        self.experts = self.experts.to(dev).to(torch.int32)
+        self._structs = {name: _proj_struct(getattr(self, name), self.bits) for name in PROJS}
+        return self
+
+    def struct(self, name: str) -> _lib.HexProj:
+        s = self._structs.get(name)
+        if s is None:
+            raise ValueError("HexTier.prepare(num_experts) has not been called")
+        return s
+
+
+# --------------------------------------------------------------------------- slot plan
+
+
+def _ids_arg(ids: torch.Tensor) -> tuple[torch.Tensor, int]:
+    if ids.dtype not in (torch.int32, torch.int64):
+        ids = ids.long()
+    ids = ids.reshape(-1).contiguous()
+    return ids, _lib.dtype_code(ids.dtype)
+
+
+def align(ids: torch.Tensor, n: int, block_m: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Group slots by expert, each expert's run padded to block_m, without a host sync
+    (hex_moe.py:201-222): sorted slot ids int32 [B * block_m] (S = padding), the expert of every
+    block int32 [B] (-1 = unused), the padded length int32 [1]; B = ceil(S/block_m) + min(n, S)."""
+    lib = _lib.load()
+    _lib.require_gpu(ids)
+    ids, code = _ids_arg(ids)
+    S = ids.numel()
+    nb = lib.bh_hex_align_max_blocks(S, n, block_m)
+    if nb < 0:
+        raise ValueError(f"bad align sizes S={S} n={n} block_m={block_m}")
+    dev = ids.device
+    sid = torch.empty(nb * block_m, dtype=torch.int32, device=dev)
+    eid = torch.empty(nb, dtype=torch.int32, device=dev)
+    npp = torch.empty(1, dtype=torch.int32, device=dev)
+    _lib.check(lib.bh_hex_align(ids.data_ptr(), code, S, n, block_m, sid.data_ptr(), eid.data_ptr(), npp.data_ptr(),
+                                _lib.stream_of(ids)), "bh_hex_align")
+    return sid, eid, npp
+
+
+def direct(ids: torch.Tensor, block_m: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """One block per slot, no sorting (hex_moe.py:228-237). Same outputs as align()."""
+    lib = _lib.load()
+    _lib.require_gpu(ids)
+    ids, code = _ids_arg(ids)
+    S = ids.numel()
+    dev = ids.device
+    sid = torch.empty(S * block_m, dtype=torch.int32, device=dev)
+    eid = torch.empty(S, dtype=torch.int32, device=dev)
+    npp = torch.empty(1, dtype=torch.int32, device=dev)
+    _lib.check(lib.bh_hex_direct(ids.data_ptr(), code, S, block_m, sid.data_ptr(), eid.data_ptr(), npp.data_ptr(),
+                                 _lib.stream_of(ids)), "bh_hex_direct")
+    return sid, eid, npp
+
+
+def plan(ids: torch.Tensor, n: int, block_m: int, mode: str = "auto"):
+    """(sorted slot ids, block experts, padded length) for the fused kernels (hex_moe.py:248-257):
+    direct for at most DIRECT_MAX slots (or mode="direct"), else the align kernel. The reference's
+    "vllm" and "torch" modes name other sorts with the same outputs; both map to the align kernel."""
+    if mode not in ("auto", "direct", "vllm", "torch"):
+        raise ValueError(f"unknown plan mode {mode!r}")
+    if mode == "direct" or (mode == "auto" and ids.numel() <= DIRECT_MAX):
+        return direct(ids, block_m)
+    return align(ids, n, block_m)
+
+
+# --------------------------------------------------------------------------- tiles
+
+
+def _tile_from(cfg: dict) -> tuple[int, int]:
+    """(block_m, k_split) of a config dict. BLOCK_M (slots per expert block) rounds to 16, 32 or
+    64; BLOCK_N (output rows per workgroup) 64, 32 or 16 means k_split 1, 2 or 4 (waves
+    splitting the inputs). The reference's BLOCK_K, num_warps and num_stages have no
+    counterpart here and are ignored."""
+    bm = int(cfg.get("BLOCK_M", 16))
+    bm = 16 if bm <= 16 else (32 if bm <= 32 else 64)
+    ks = cfg.get("K_SPLIT")
+    if ks is None:
+        bn = int(cfg.get("BLOCK_N", 64))
+        ks = 4 if bn <= 16 else (2 if bn <= 32 else 1)
+    ks = int(ks)
+    if ks not in (1, 2, 4):
+        raise ValueError(f"K_SPLIT must be 1, 2 or 4, got {ks}")
+    return bm, ks
+
+
+def default_config(slots: int, n_out: int, n_in: int, glu: bool, n_experts: int = 0) -> dict:
+    """Tile choice by slot count (hex_moe.py:264-283), or BLACKHOLE_HEX_TILES="BM,BN[,KS]".
+    BLOCK_M grows with the slots each expert gets, so an expert's weights are streamed by few
+    blocks; K_SPLIT splits the inputs over the workgroup's waves when too few (expert block,
+    row tile) pairs would otherwise fill the 256 compute units."""
+    env = os.environ.get("BLACKHOLE_HEX_TILES")
+    if env:
+        v = [int(t) for t in env.split(",")]
+        cfg = dict(zip(("BLOCK_M", "BLOCK_N", "K_SPLIT"), v))
+        bm, ks = _tile_from(cfg)
+        return {"BLOCK_M": bm, "BLOCK_N": 64 // ks, "K_SPLIT": ks}
+    per_expert = slots / max(1, n_experts or slots)
+    bm = 16 if per_expert <= 16 else (32 if per_expert <= 48 else 64)
+    if glu and bm == 64:
+        bm = 32      # the 4-subtile SwiGLU variant spills at 128-input scale blocks
+    blocks = min(slots, n_experts or slots)
+    ks = 1
+    while ks < 4 and blocks * -(-n_out // (64 // ks)) < 1024:
+        ks *= 2
+    return {"BLOCK_M": bm, "BLOCK_N": 64 // ks, "K_SPLIT": ks}
+
+
+# --------------------------------------------------------------------------- fused path
+
+
+def _launch_glu(x, act, t: HexTier, sid, eid, npp, S, a_div, bm, ks):
+    lib = _lib.load()
+    n_out = t.gate_proj["idx"].shape[1]
+    n_in = _n_in(t.gate_proj, t.bits)
+    assert x.shape[1] == n_in, f"input width {x.shape[1]} != HEX width {n_in}"
+    tile = _lib.HexTile(bm, 64 // ks, ks)
+    _lib.check(lib.bh_hex_moe_glu(
+        x.data_ptr(), _lib.dtype_code(x.dtype), x.stride(0), act.data_ptr(), act.stride(0),
+        t.struct("gate_proj"), t.struct("up_proj"), t.bits, n_out, n_in,
+        sid.data_ptr(), eid.data_ptr(), eid.numel(), npp.data_ptr(), t.lookup.data_ptr(), t.lookup.numel(), S, a_div,
+        tile, _lib.stream_of(x)), "bh_hex_moe_glu")
+
+
+def _launch_down(act, y, t: HexTier, sid, eid, npp, S, w, bm, ks):
+    lib = _lib.load()
+    n_out = t.down_proj["idx"].shape[1]
+    n_in = _n_in(t.down_proj, t.bits)
+    assert act.shape[1] == n_in, f"input width {act.shape[1]} != HEX width {n_in}"
+    tile = _lib.HexTile(bm, 64 // ks, ks)
+    _lib.check(lib.bh_hex_moe_down(
+        act.data_ptr(), _lib.dtype_code(act.dtype), act.stride(0), y.data_ptr(), y.stride(0),
+        t.struct("down_proj"), t.bits, n_out, n_in,
+        sid.data_ptr(), eid.data_ptr(), eid.numel(), npp.data_ptr(), t.lookup.data_ptr(), t.lookup.numel(), S,
+        w.data_ptr(), tile, _lib.stream_of(act)), "bh_hex_moe_down")
+
+
+def _covers_all(tiers: list[HexTier]) -> bool:
+    """Whether every expert id has a tier (then every slot's y row is written by a kernel)."""
+    seen = torch.zeros(tiers[0].lookup.numel(), dtype=torch.bool)
+    for t in tiers:
+        if t._experts_host is None:
+            raise ValueError("HexTier.prepare(num_experts) has not been called")
+        seen[t._experts_host] = True
+    return bool(seen.all())
+
+
+def hex_moe_fused(x, topk_weights, topk_ids, tiers: list[HexTier], config: dict | None = None,
+                  align_mode: str = "auto") -> torch.Tensor:
+    """Routed-expert output [T, H] in x.dtype through the fused HIP kernels (hex_moe.py:304-325).
+    x bf16 or f16 [T, H]; topk_weights [T, k]; topk_ids int [T, k]; tiers prepared."""
+    if not tiers:
+        raise ValueError("no HEX tiers")
+    _lib.require_gpu(x, topk_weights, topk_ids)
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise NotImplementedError(f"the fused HEX kernels take bf16 or f16 activations, got {x.dtype} "
+                                  "(use path='dequant')")
+    T, k = topk_ids.shape
+    S = T * k
+    H = x.shape[1]
+    I = tiers[0].gate_proj["idx"].shape[1]
+    E = tiers[0].lookup.numel()
+    x = x.contiguous()
+    out = torch.empty(T, H, dtype=x.dtype, device=x.device)
+    if T == 0:
+        return out
+    flat = topk_ids.reshape(-1)
+    w = topk_weights.reshape(-1).float().contiguous()
+    act = torch.empty(S, I, dtype=x.dtype, device=x.device)
+    y = (torch.empty if _covers_all(tiers) else torch.zeros)(S, H, dtype=torch.float32, device=x.device)
+    c1 = config or default_config(S, I, H, True, E)
+    c2 = config or default_config(S, H, I, False, E)
+    bm1, ks1 = _tile_from(c1)
+    bm2, ks2 = _tile_from(c2)
+    p1 = plan(flat, E, bm1, align_mode)
+    p2 = p1 if bm2 == bm1 else plan(flat, E, bm2, align_mode)
+    for t in tiers:
+        _launch_glu(x, act, t, *p1, S, k, bm1, ks1)
+    for t in tiers:
+        _launch_down(act, y, t, *p2, S, w, bm2, ks2)
+    ids, code = _ids_arg(flat)
+    lib = _lib.load()
+    _lib.check(lib.bh_hex_moe_reduce(y.data_ptr(), y.stride(0), ids.data_ptr(), code, E, T, k, H, out.data_ptr(),
+                                     _lib.dtype_code(out.dtype), out.stride(0), _lib.stream_of(x)), "bh_hex_moe_reduce")
+    return out
+
+
+# --------------------------------------------------------------------------- dequant path
+
+
+def hex_dequant(idx, block_scale, expert_scale, levels, bits: int, order: str = "R",
+                dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """Weights [n, out, in] from stacked HEX parts on the GPU, in the named association order:
+    "R" level * (fp8 * es) (blackhole/anatomy/hex.py:180-204), "D" (level * fp8) * es (the
+    reference's dequant kernel, hex_moe.py:163-164), "T" bf16(level * fp8) (its fused operand)."""
+    lib = _lib.load()
+    _lib.require_gpu(idx, block_scale, expert_scale, levels)
+    idx = idx.view(torch.int32) if idx.dtype == torch.uint32 else idx
+    n, n_out = idx.shape[0], idx.shape[1]
+    p = {"idx": idx.contiguous(), "block_scale": block_scale.contiguous(),
+         "expert_scale": expert_scale.float().reshape(-1).contiguous(), "levels": levels.float().contiguous()}
+    n_in = _n_in(p, bits)
+    out = torch.empty(n, n_out, n_in, dtype=dtype, device=idx.device)
+    code = {"R": _lib.ORDER_R, "D": _lib.ORDER_D, "T": _lib.ORDER_T}[order]
+    _lib.check(lib.bh_hex_dequant(_proj_struct(p, bits), bits, n, n_out, n_in, None, out.data_ptr(),
+                                  _lib.dtype_code(dtype), out.stride(0), out.stride(1), 0, code,
+                                  _lib.stream_of(idx)), "bh_hex_dequant")
+    return out
+
+
+def dequant_all(tiers: list[HexTier], dtype=torch.bfloat16, order: str = "D") -> tuple[torch.Tensor, torch.Tensor]:
+    """All experts as stacks: w13 [E, 2I, H] (gate rows, then up) and w2 [E, H, I]
+    (hex_moe.py:328-346), in the reference dequant kernel's order "D" by default."""
+    lib = _lib.load()
+    t0 = tiers[0]
+    E = t0.lookup.numel()
+    I = t0.gate_proj["idx"].shape[1]
+    H = _n_in(t0.gate_proj, t0.bits)
+    dev = t0.gate_proj["idx"].device
+    w13 = torch.empty(E, 2 * I, H, dtype=dtype, device=dev)
+    w2 = torch.empty(E, H, I, dtype=dtype, device=dev)
+    code = {"R": _lib.ORDER_R, "D": _lib.ORDER_D, "T": _lib.ORDER_T}[order]
+    st = _lib.stream_of(w13)
+    for t in tiers:
+        n = len(t.experts)
+        for name, out, row_off in (("gate_proj", w13, 0), ("up_proj", w13, I), ("down_proj", w2, 0)):
+            p = getattr(t, name)
+            N, K = p["idx"].shape[1], _n_in(p, t.bits)
+            _lib.check(lib.bh_hex_dequant(t.struct(name), t.bits, n, N, K, t.experts.data_ptr(), out.data_ptr(),
+                                          _lib.dtype_code(dtype), out.stride(0), out.stride(1), row_off, code, st),
+                       "bh_hex_dequant")
+    return w13, w2
+
+
+def hex_moe_dequant(x, topk_weights, topk_ids, tiers: list[HexTier]) -> torch.Tensor:
+    """Routed-expert output [T, H]: every expert decoded once (dequant kernel), then per routed
+    expert gate/up and down products in the weights' dtype (hex_moe.py:357-371; vLLM's bf16
+    fused MoE is not part of this build, so the products go through torch's GEMM per expert).
+    The activation is handed to the down product in x.dtype, as the reference's kernels do."""
+    _lib.require_gpu(x, topk_weights, topk_ids)
+    wdt = x.dtype if x.dtype in (torch.bfloat16, torch.float16) else torch.float32
+    w13, w2 = dequant_all(tiers, wdt)
+    T, k = topk_ids.shape
+    I = w2.shape[-1]
+    out = torch.zeros(T, x.shape[1], dtype=torch.float32, device=x.device)
+    xw = x.to(wdt)
+    ids = topk_ids.long()
+    for e in torch.unique(ids).tolist():
+        tok, slot = (ids == e).nonzero(as_tuple=True)
+        h = torch.nn.functional.linear(xw[tok], w13[e]).float()
+        a = (torch.nn.functional.silu(h[:, :I]) * h[:, I:]).to(x.dtype).to(wdt)
+        out.index_add_(0, tok, torch.nn.functional.linear(a, w2[e]).float() * topk_weights[tok, slot, None].float())
+    return out.to(x.dtype)
+
+
+def hex_moe(x: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor, tiers: list[HexTier],
+            config: dict | None = None, path: str = "auto") -> torch.Tensor:
+    """Routed-expert output [T, H] of a SwiGLU MoE layer whose experts are HEX tiers (prepared)
+    (hex_moe.py:374-382). path: "auto" (fused below DEQUANT_MIN slots, else dequant, never
+    dequant while capturing a graph; float32 activations always dequant), "fused" or "dequant"."""
+    if path not in ("auto", "fused", "dequant"):
+        raise ValueError(f"unknown path {path!r}")
+    capturing = x.is_cuda and torch.cuda.is_current_stream_capturing()
+    if path == "dequant" or (path == "auto" and x.dtype == torch.float32) or (
+            path == "auto" and config is None and not capturing and topk_ids.numel() >= DEQUANT_MIN):
+        return hex_moe_dequant(x, topk_weights, topk_ids, tiers)
+    return hex_moe_fused(x, topk_weights, topk_ids, tiers, config)
+
+
+# --------------------------------------------------------------------------- routing
+
+
+def route_topk(logits: torch.Tensor, k: int, renormalize: bool = True,
+               ids_dtype: torch.dtype = torch.int64) -> tuple[torch.Tensor, torch.Tensor]:
+    """Softmax routing on the GPU (reaper/reaper_pipeline/moe.py:161-166, softmax branch):
+    (weights float32 [T, k] in descending order, ids [T, k])."""
+    lib = _lib.load()
+    _lib.require_gpu(logits)
+    if logits.stride(-1) != 1:
+        logits = logits.contiguous()
+    T, E = logits.shape
+    w = torch.empty(T, k, dtype=torch.float32, device=logits.device)
+    ids = torch.empty(T, k, dtype=ids_dtype, device=logits.device)
+    _lib.check(lib.bh_hex_route_topk(logits.data_ptr(), _lib.dtype_code(logits.dtype), logits.stride(0), T, E, k,
+                                     int(renormalize), w.data_ptr(), ids.data_ptr(), _lib.dtype_code(ids_dtype),
+                                     _lib.stream_of(logits)), "bh_hex_route_topk")
+    return w, ids

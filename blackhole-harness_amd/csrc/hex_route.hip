@@ -1,0 +1,308 @@
+// Routing and slot planning for the HEX MoE kernels.
+//
+//   bh_hex_route_topk  softmax -> top-k -> renormalise, one wave per token
+//                      (reaper/reaper_pipeline/moe.py:161-166, softmax branch)
+//   bh_hex_align       stable counting sort of slots by expert, padded to block_m
+//                      (runtime/blackhole_runtime/hex_moe.py:201-222)
+//   bh_hex_direct      one block per slot (hex_moe.py:228-237)
+//
+// align runs in one workgroup of 1024 threads. Counts come from LDS atomics; the order of slots
+// inside an expert's run is the slot order (the reference's stable argsort). Each wave finds,
+// for each of its 64 slots, the lanes holding the same expert by intersecting one ballot per bit
+// of the expert id (log2(E) ballots, independent of how many experts the wave holds); the
+// slot's rank inside its run is then the run's offset so far + the counts of earlier waves of
+// the chunk + the same-expert lanes below it.
+#include <string>
+
+#include "hex_common.h"
+
+namespace bh {
+
+// ----------------------------------------------------------------------------------- top-k
+
+template <int LDT>
+__device__ __forceinline__ float load_logit(const void* p, int64_t i) {
+  if constexpr (LDT == BH_HEX_F32) return reinterpret_cast<const float*>(p)[i];
+  else if constexpr (LDT == BH_HEX_BF16) return bf16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+  else return f16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+}
+
+constexpr int kTopkPerLane = 16;   // up to 1024 experts
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+
+template <int LDT, int IDT>
+__global__ __launch_bounds__(256) void route_topk_kernel(const void* __restrict__ logits, int64_t s_lt, int64_t T,
+                                                         int32_t E, int32_t k, int32_t renorm,
+                                                         float* __restrict__ topk_w, void* __restrict__ topk_ids) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  float p[kTopkPerLane];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < kTopkPerLane; ++j) {
+    const int e = lane + kWave * j;
+    p[j] = e < E ? load_logit<LDT>(logits, t * s_lt + e) : -INFINITY;
+    mx = fmaxf(mx, p[j]);
+  }
+  mx = wave_max(mx);
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < kTopkPerLane; ++j) {
+    const int e = lane + kWave * j;
+    p[j] = e < E ? expf(p[j] - mx) : 0.f;
+    s += p[j];
+  }
+  s = wave_sum(s);
+#pragma unroll
+  for (int j = 0; j < kTopkPerLane; ++j) {
+    const int e = lane + kWave * j;
+    p[j] = e < E ? p[j] / s : -1.f;      // probabilities; -1 never wins
+  }
+  float wsel = 0.f, wsum = 0.f;
+  int isel = 0;
+  for (int r = 0; r < k; ++r) {
+    // this lane's best (largest value, then lowest expert id)
+    float bv = -2.f;
+    int bi = 0x7FFFFFFF;
+#pragma unroll
+    for (int j = 0; j < kTopkPerLane; ++j) {
+      const int e = lane + kWave * j;
+      if (p[j] > bv) { bv = p[j]; bi = e; }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+      const float ov = __shfl_xor(bv, m, kWave);
+      const int oi = __shfl_xor(bi, m, kWave);
+      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+#pragma unroll
+    for (int j = 0; j < kTopkPerLane; ++j)
+      if (lane + kWave * j == bi) p[j] = -2.f;
+    wsum += bv;
+    if (lane == r) { wsel = bv; isel = bi; }
+  }
+  if (lane < k) {
+    const float w = renorm ? wsel / wsum : wsel;
+    topk_w[t * k + lane] = w;
+    if constexpr (IDT == BH_HEX_I64) reinterpret_cast<int64_t*>(topk_ids)[t * k + lane] = isel;
+    else reinterpret_cast<int32_t*>(topk_ids)[t * k + lane] = isel;
+  }
+}
+
+// ----------------------------------------------------------------------------------- align
+
+constexpr int kAlignThreads = 1024;
+constexpr int kAlignWaves = kAlignThreads / kWave;
+constexpr int kAlignMaxExperts = 1024;
+
+template <int IDT>
+__device__ __forceinline__ int64_t load_id(const void* p, int64_t i) {
+  if constexpr (IDT == BH_HEX_I64) return reinterpret_cast<const int64_t*>(p)[i];
+  else return reinterpret_cast<const int32_t*>(p)[i];
+}
+
+// Inclusive prefix sum over the workgroup of one value per thread (1024 threads).
+__device__ int block_incl_scan(int v, int* wsum) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int o = __shfl_up(v, d, kWave);
+    if (lane >= d) v += o;
+  }
+  if (lane == kWave - 1) wsum[w] = v;
+  __syncthreads();
+  if (w == 0) {
+    int s = lane < kAlignWaves ? wsum[lane] : 0;
+#pragma unroll
+    for (int d = 1; d < kAlignWaves; d <<= 1) {
+      const int o = __shfl_up(s, d, kWave);
+      if (lane >= d) s += o;
+    }
+    if (lane < kAlignWaves) wsum[lane] = s;
+  }
+  __syncthreads();
+  const int r = v + (w ? wsum[w - 1] : 0);
+  __syncthreads();
+  return r;
+}
+
+template <int IDT>
+__global__ __launch_bounds__(kAlignThreads) void align_kernel(const void* __restrict__ ids, int64_t S, int32_t n,
+                                                              int32_t bm, int64_t max_blocks,
+                                                              int32_t* __restrict__ sorted_ids,
+                                                              int32_t* __restrict__ expert_ids,
+                                                              int32_t* __restrict__ npp) {
+  __shared__ int cnt[kAlignMaxExperts];      // slots per expert, then the running offset
+  __shared__ int start[kAlignMaxExperts];    // first padded row of the expert's run
+  __shared__ int wcnt[kAlignWaves][kAlignMaxExperts];
+  __shared__ int wsum[kAlignWaves];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+
+  for (int e = tid; e < n; e += kAlignThreads) cnt[e] = 0;
+  __syncthreads();
+  for (int64_t i = tid; i < S; i += kAlignThreads) {
+    const int64_t e = load_id<IDT>(ids, i);
+    if (e >= 0 && e < n) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+
+  // blocks per expert -> block ends (inclusive scan over experts, each thread a run of them)
+  const int per = (n + kAlignThreads - 1) / kAlignThreads;
+  const int e0 = tid * per, e1 = min(n, e0 + per);
+  int local = 0;
+  for (int e = e0; e < e1; ++e) local += (cnt[e] + bm - 1) / bm;
+  const int incl = block_incl_scan(local, wsum);
+  int run = incl - local;                      // blocks before this thread's experts
+  for (int e = e0; e < e1; ++e) {
+    const int nb = (cnt[e] + bm - 1) / bm;
+    start[e] = run * bm;
+    for (int b = run; b < run + nb; ++b) expert_ids[b] = e;
+    // rows of the run that no slot fills
+    for (int64_t r = (int64_t)run * bm + cnt[e]; r < (int64_t)(run + nb) * bm; ++r) sorted_ids[r] = (int32_t)S;
+    run += nb;
+  }
+  __shared__ int total_blocks;
+  if (tid == kAlignThreads - 1) total_blocks = incl;
+  __syncthreads();
+  const int used = total_blocks;
+  for (int64_t b = used + tid; b < max_blocks; b += kAlignThreads) expert_ids[b] = -1;
+  for (int64_t r = (int64_t)used * bm + tid; r < max_blocks * bm; r += kAlignThreads) sorted_ids[r] = (int32_t)S;
+  if (tid == 0) npp[0] = used * bm;
+  for (int e = tid; e < n; e += kAlignThreads) cnt[e] = 0;   // now the running offset
+  __syncthreads();
+
+  // stable scatter, one chunk of 1024 slots at a time
+  int nbits = 1;
+  while ((1 << nbits) <= n) ++nbits;          // ids in [0, n] (n marks "not placed")
+  const uint64_t below = (lane ? (~0ull >> (64 - lane)) : 0ull);
+  for (int64_t c0 = 0; c0 < S; c0 += kAlignThreads) {
+    for (int i = tid; i < kAlignWaves * n; i += kAlignThreads) (&wcnt[0][0])[i] = 0;
+    const int64_t i = c0 + tid;
+    int key = n;
+    if (i < S) {
+      const int64_t e = load_id<IDT>(ids, i);
+      if (e >= 0 && e < n) key = (int)e;
+    }
+    uint64_t same = ~0ull;
+    for (int b = 0; b < nbits; ++b) {
+      const bool bit = (key >> b) & 1;
+      const uint64_t bal = __ballot(bit);
+      same &= bit ? bal : ~bal;
+    }
+    const int rank = __popcll(same & below);
+    __syncthreads();
+    if (key < n && rank == 0) wcnt[w][key] = __popcll(same);
+    __syncthreads();
+    for (int e = tid; e < n; e += kAlignThreads) {       // exclusive prefix over the waves
+      int acc = cnt[e];
+      for (int v = 0; v < kAlignWaves; ++v) {
+        const int c = wcnt[v][e];
+        wcnt[v][e] = acc;
+        acc += c;
+      }
+      cnt[e] = acc;
+    }
+    __syncthreads();
+    if (key < n) sorted_ids[start[key] + wcnt[w][key] + rank] = (int32_t)i;
+    __syncthreads();
+  }
+}
+
+template <int IDT>
+__global__ __launch_bounds__(256) void direct_kernel(const void* __restrict__ ids, int64_t S, int32_t bm,
+                                                     int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids,
+                                                     int32_t* __restrict__ npp) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r < S * bm) {
+    const int64_t s = r / bm;
+    sorted_ids[r] = (r - s * bm) == 0 ? (int32_t)s : (int32_t)S;
+  }
+  if (r < S) expert_ids[r] = (int32_t)load_id<IDT>(ids, r);
+  if (r == 0) npp[0] = (int32_t)(S * bm);
+}
+
+}  // namespace bh
+
+using namespace bh;
+
+extern "C" int bh_hex_route_topk(const void* logits, int32_t logits_dtype, int64_t s_lt, int64_t T, int32_t E, int32_t k,
+                                 int32_t renormalize, float* topk_w, void* topk_ids, int32_t ids_dtype, void* stream) {
+  if (T < 0) return fail(BH_HEX_ERR_VALUE, "bh_hex_route_topk: negative token count");
+  if (E <= 0 || E > kWave * kTopkPerLane)
+    return fail(BH_HEX_ERR_UNSUPPORTED, "bh_hex_route_topk: experts must be in 1.." + std::to_string(kWave * kTopkPerLane));
+  if (k <= 0 || k > E || k > kWave) return fail(BH_HEX_ERR_VALUE, "bh_hex_route_topk: k must be in 1..min(E, 64)");
+  if (ids_dtype != BH_HEX_I32 && ids_dtype != BH_HEX_I64)
+    return fail(BH_HEX_ERR_UNSUPPORTED, "bh_hex_route_topk: ids dtype must be I32 or I64");
+  if (T == 0) return BH_HEX_OK;
+  if (!logits || !topk_w || !topk_ids) return fail(BH_HEX_ERR_VALUE, "bh_hex_route_topk: null pointer");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)cdiv(T, 4));
+#define BH_ROUTE(LDT, IDT)                                                                                         \
+  hipLaunchKernelGGL((route_topk_kernel<LDT, IDT>), grid, dim3(256), 0, st, logits, s_lt, T, E, k, renormalize, topk_w, \
+                     topk_ids)
+  if (logits_dtype == BH_HEX_F32) {
+    if (ids_dtype == BH_HEX_I64) BH_ROUTE(BH_HEX_F32, BH_HEX_I64); else BH_ROUTE(BH_HEX_F32, BH_HEX_I32);
+  } else if (logits_dtype == BH_HEX_BF16) {
+    if (ids_dtype == BH_HEX_I64) BH_ROUTE(BH_HEX_BF16, BH_HEX_I64); else BH_ROUTE(BH_HEX_BF16, BH_HEX_I32);
+  } else if (logits_dtype == BH_HEX_F16) {
+    if (ids_dtype == BH_HEX_I64) BH_ROUTE(BH_HEX_F16, BH_HEX_I64); else BH_ROUTE(BH_HEX_F16, BH_HEX_I32);
+  } else {
+    return fail(BH_HEX_ERR_UNSUPPORTED, "bh_hex_route_topk: logits dtype must be F32, BF16 or F16");
+  }
+#undef BH_ROUTE
+  return check_launch("bh_hex_route_topk");
+}
+
+extern "C" int64_t bh_hex_align_max_blocks(int64_t S, int32_t n_experts, int32_t block_m) {
+  if (block_m <= 0 || S < 0 || n_experts < 0) return -1;
+  return cdiv(S, block_m) + (S < n_experts ? S : (int64_t)n_experts);
+}
+
+extern "C" int bh_hex_align(const void* ids, int32_t ids_dtype, int64_t S, int32_t n_experts, int32_t block_m,
+                            int32_t* sorted_ids, int32_t* expert_ids, int32_t* npp, void* stream) {
+  if (block_m <= 0) return fail(BH_HEX_ERR_VALUE, "bh_hex_align: block_m must be positive");
+  if (n_experts <= 0 || n_experts > kAlignMaxExperts)
+    return fail(BH_HEX_ERR_UNSUPPORTED, "bh_hex_align: experts must be in 1.." + std::to_string(kAlignMaxExperts));
+  if (S < 0 || S > (int64_t)INT32_MAX / 2) return fail(BH_HEX_ERR_VALUE, "bh_hex_align: slot count out of range");
+  if (ids_dtype != BH_HEX_I32 && ids_dtype != BH_HEX_I64)
+    return fail(BH_HEX_ERR_UNSUPPORTED, "bh_hex_align: ids dtype must be I32 or I64");
+  if (!npp || (S > 0 && (!ids || !sorted_ids || !expert_ids))) return fail(BH_HEX_ERR_VALUE, "bh_hex_align: null pointer");
+  const int64_t max_blocks = bh_hex_align_max_blocks(S, n_experts, block_m);
+  if (max_blocks * block_m > (int64_t)INT32_MAX) return fail(BH_HEX_ERR_VALUE, "bh_hex_align: plan too large");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (ids_dtype == BH_HEX_I64)
+    hipLaunchKernelGGL((align_kernel<BH_HEX_I64>), dim3(1), dim3(kAlignThreads), 0, st, ids, S, n_experts, block_m,
+                       max_blocks, sorted_ids, expert_ids, npp);
+  else
+    hipLaunchKernelGGL((align_kernel<BH_HEX_I32>), dim3(1), dim3(kAlignThreads), 0, st, ids, S, n_experts, block_m,
+                       max_blocks, sorted_ids, expert_ids, npp);
+  return check_launch("bh_hex_align");
+}
+
+extern "C" int bh_hex_direct(const void* ids, int32_t ids_dtype, int64_t S, int32_t block_m, int32_t* sorted_ids,
+                             int32_t* expert_ids, int32_t* npp, void* stream) {
+  if (block_m <= 0) return fail(BH_HEX_ERR_VALUE, "bh_hex_direct: block_m must be positive");
+  if (S < 0 || S * block_m > (int64_t)INT32_MAX) return fail(BH_HEX_ERR_VALUE, "bh_hex_direct: slot count out of range");
+  if (ids_dtype != BH_HEX_I32 && ids_dtype != BH_HEX_I64)
+    return fail(BH_HEX_ERR_UNSUPPORTED, "bh_hex_direct: ids dtype must be I32 or I64");
+  if (!npp || (S > 0 && (!ids || !sorted_ids || !expert_ids))) return fail(BH_HEX_ERR_VALUE, "bh_hex_direct: null pointer");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int64_t work = S * block_m > 0 ? S * block_m : 1;
+  const dim3 grid((unsigned)cdiv(work, 256));
+  if (ids_dtype == BH_HEX_I64)
+    hipLaunchKernelGGL((direct_kernel<BH_HEX_I64>), grid, dim3(256), 0, st, ids, S, block_m, sorted_ids, expert_ids, npp);
+  else
+    hipLaunchKernelGGL((direct_kernel<BH_HEX_I32>), grid, dim3(256), 0, st, ids, S, block_m, sorted_ids, expert_ids, npp);
+  return check_launch("bh_hex_direct");
+}

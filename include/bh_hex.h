@@ -1,0 +1,147 @@
+/*
+ * bh_hex.h: C ABI of the MI355X (gfx950) HEX fused-MoE library, libbh_hex.so.
+ *
+ * HEX ("Header-Encoded eXperts") stores each expert matrix W [out, in] as
+ *   idx           uint32 [n, out, in / 32 * bits]  one little-endian bit stream per 32 inputs
+ *   block_scale   uint8  [n, out, in / B]          fp8 e4m3 code per block of B inputs (32 or 128)
+ *   expert_scale  float  [n]
+ *   levels        float  [n, 2^bits]               the expert's own sorted level table
+ *   W[e, o, i] = levels[e, code] * fp8(block_scale[e, o, i / B]) * expert_scale[e]
+ * (reference layout: blackhole/anatomy/hex.py:21-31, runtime/blackhole_runtime/hex_ref.py:5-11).
+ * fp8 codes decode by the kernels' formula: 0x7F / 0xFF give +-480, not NaN.
+ *
+ * Conventions for every entry point:
+ *   - all pointers are device pointers (HIP), owned by the caller; the library keeps none of
+ *     them after it returns and allocates no device memory;
+ *   - strides are in elements; the innermost dimension of every tensor is contiguous;
+ *   - work is enqueued on `stream` (a hipStream_t; NULL is the default stream) and nothing
+ *     synchronises the host, so every entry point can be captured in a hipGraph;
+ *   - the return value is a status code; bh_hex_last_error() gives the message of the last
+ *     failing call on the calling thread. BH_HEX_ERR_VALUE corresponds to the reference's
+ *     ValueError, BH_HEX_ERR_ASSERT to its AssertionError (width checks).
+ * Calls that overlap on one stream are ordered; calls on different streams writing the same
+ * output race, as any two kernels would.
+ */
+#ifndef BH_HEX_H
+#define BH_HEX_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BH_HEX_ABI_VERSION 1
+
+enum bh_hex_status {
+  BH_HEX_OK = 0,
+  BH_HEX_ERR_VALUE = 1,       /* bad argument or shape (reference: ValueError) */
+  BH_HEX_ERR_ASSERT = 2,      /* width check (reference: AssertionError, hex_moe.py:289-290) */
+  BH_HEX_ERR_HIP = 3,         /* the HIP runtime refused a launch */
+  BH_HEX_ERR_UNSUPPORTED = 4  /* a dtype / bits / block combination this build has no kernel for */
+};
+
+enum bh_hex_dtype { BH_HEX_F32 = 0, BH_HEX_BF16 = 1, BH_HEX_F16 = 2, BH_HEX_I32 = 3, BH_HEX_I64 = 4 };
+
+/* Association orders of the dequantized value (each product rounded once to float32):
+ *   R  level * (fp8 * es)   torch/numpy source of truth   (blackhole/anatomy/hex.py:180-204, 116-123)
+ *   D  (level * fp8) * es   the reference's dequant kernel (runtime/blackhole_runtime/hex_moe.py:163-164)
+ *   T  bf16(level * fp8)    the operand of its fused kernel, no expert scale (hex_moe.py:105, 140) */
+enum bh_hex_order { BH_HEX_ORDER_R = 0, BH_HEX_ORDER_D = 1, BH_HEX_ORDER_T = 2 };
+
+/* One projection (gate_proj, up_proj or down_proj) of one tier: the HexTier part dict of
+ * runtime/blackhole_runtime/hex_moe.py:174-198 after prepare(). */
+typedef struct bh_hex_proj {
+  const uint32_t* idx;          /* [n, out, in / 32 * bits]                         */
+  const uint8_t* block_scale;   /* [n, out, in / block]                             */
+  const float* expert_scale;    /* [n]                                              */
+  const float* levels;          /* [n, 2^bits], contiguous                          */
+  int64_t s_ie, s_in;           /* idx strides of dims 0 and 1                      */
+  int64_t s_be, s_bn;           /* block_scale strides of dims 0 and 1              */
+  int32_t block;                /* inputs per fp8 scale: in / block_scale.shape[-1],
+                                   a multiple of 32 (the reference writes 32)       */
+} bh_hex_proj;
+
+/* Tile choice of the fused kernels (the config dict of hex_moe.py:264-283, CDNA4 terms):
+ * block_m slots per expert block (a multiple of 16), block_n output rows per workgroup
+ * (a multiple of 16), k_split waves sharing one output tile along the input dimension
+ * (1, 2 or 4). */
+typedef struct bh_hex_tile {
+  int32_t block_m;
+  int32_t block_n;
+  int32_t k_split;
+} bh_hex_tile;
+
+/* Message of the last failing call on this thread ("" when none). */
+const char* bh_hex_last_error(void);
+int bh_hex_abi_version(void);
+
+/* Dequantize one tier projection into a stacked output, one float per weight:
+ *   out[expert_ids[e], row_off + o, i] = W[e, o, i] in association order `order`,
+ * rounded to out_dtype (F32, BF16 or F16) to nearest even.
+ * n experts of the tier, n_out rows, n_in inputs (a multiple of 32 and of the block).
+ * Replaces _hex_dequant_kernel and its launch in dequant_all (hex_moe.py:154-168, 328-346) and
+ * hex_dequant (blackhole/anatomy/hex.py:180-204) when expert_ids is the identity. */
+int bh_hex_dequant(const bh_hex_proj* w, int32_t bits, int64_t n, int64_t n_out, int64_t n_in,
+                   const int32_t* expert_ids, void* out, int32_t out_dtype, int64_t s_oe, int64_t s_on,
+                   int64_t row_off, int32_t order, void* stream);
+
+/* Softmax routing of router logits [T, E] (fp32, bf16 or f16; row stride s_lt): the k largest
+ * probabilities in descending order (ties to the lower expert), optionally divided by their sum.
+ * topk_w float [T, k]; topk_ids [T, k] in ids_dtype (I32 or I64).
+ * Upstream of the plugin boundary: the statement of reaper/reaper_pipeline/moe.py:161-166
+ * (softmax branch), as vLLM computes it before HexMoEMethod.apply (vllm_hex.py:239-240). */
+int bh_hex_route_topk(const void* logits, int32_t logits_dtype, int64_t s_lt, int64_t T, int32_t E, int32_t k,
+                      int32_t renormalize, float* topk_w, void* topk_ids, int32_t ids_dtype, void* stream);
+
+/* Number of expert blocks align() produces: ceil(S / block_m) + min(n_experts, S). */
+int64_t bh_hex_align_max_blocks(int64_t S, int32_t n_experts, int32_t block_m);
+
+/* Stable counting sort of S slots by expert, each expert's run padded to block_m
+ * (runtime/blackhole_runtime/hex_moe.py:201-222, align):
+ *   sorted_ids int32 [max_blocks * block_m]: slot ids grouped by expert in slot order, S as padding
+ *   expert_ids int32 [max_blocks]: the expert of each block, -1 past the last used block
+ *   npp        int32 [1]: used blocks * block_m
+ * ids (I32 or I64) outside [0, n_experts) are not placed. */
+int bh_hex_align(const void* ids, int32_t ids_dtype, int64_t S, int32_t n_experts, int32_t block_m,
+                 int32_t* sorted_ids, int32_t* expert_ids, int32_t* npp, void* stream);
+
+/* One block per slot, no sorting (hex_moe.py:228-237, direct): sorted_ids[s * block_m] = s and S
+ * elsewhere, expert_ids = ids as int32, npp = S * block_m. */
+int bh_hex_direct(const void* ids, int32_t ids_dtype, int64_t S, int32_t block_m, int32_t* sorted_ids,
+                  int32_t* expert_ids, int32_t* npp, void* stream);
+
+/* The gate/up half of a SwiGLU expert layer over one tier, for every expert block of the plan:
+ *   act[s, o] = silu(es_g * sum_i a[s] W_g[o, i]) * (es_u * sum_i a[s] W_u[o, i]),
+ *   a[s] = x[s / a_div], s the slots of the block (rows >= num_slots are padding).
+ * Blocks whose expert belongs to another tier (lookup[e] < 0) are skipped. x and act are
+ * BF16 or F16 (x_dtype; act has the same dtype), x [T, n_in], act [num_slots, n_out].
+ * Weights enter the bf16/f16 matrix cores as round(level); each 32-input block's partial sum is
+ * multiplied by its fp8 scale in float32 and the expert scale is applied at the end.
+ * Replaces _hex_moe_kernel with GLU=True and its launch (hex_moe.py:109-151, 286-301, 322). */
+int bh_hex_moe_glu(const void* x, int32_t x_dtype, int64_t s_xm, void* act, int64_t s_am,
+                   const bh_hex_proj* gate, const bh_hex_proj* up, int32_t bits, int64_t n_out, int64_t n_in,
+                   const int32_t* sorted_ids, const int32_t* expert_ids, int64_t num_blocks, const int32_t* npp,
+                   const int32_t* lookup, int32_t n_experts, int64_t num_slots, int32_t a_div,
+                   const bh_hex_tile* tile, void* stream);
+
+/* The down half over one tier: y[s, o] = (es_d * sum_i act[s, i] W_d[o, i]) * topk_w[s],
+ * written as float32 y [num_slots, n_out] (row stride s_ym) for the slots of every block of
+ * this tier's experts. Replaces _hex_moe_kernel with GLU=False, MUL_W=True (hex_moe.py:324). */
+int bh_hex_moe_down(const void* act, int32_t act_dtype, int64_t s_am, float* y, int64_t s_ym,
+                    const bh_hex_proj* down, int32_t bits, int64_t n_out, int64_t n_in,
+                    const int32_t* sorted_ids, const int32_t* expert_ids, int64_t num_blocks, const int32_t* npp,
+                    const int32_t* lookup, int32_t n_experts, int64_t num_slots, const float* topk_w,
+                    const bh_hex_tile* tile, void* stream);
+
+/* out[t, h] = sum_j y[t * k + j, h] over the token's k slots, in float32, rounded once to
+ * out_dtype (F32, BF16 or F16); slots whose id (topk_ids, I32 or I64) is outside
+ * [0, n_experts) contribute nothing. Replaces y.view(T, k, H).sum(1) (hex_moe.py:325). */
+int bh_hex_moe_reduce(const float* y, int64_t s_ym, const void* topk_ids, int32_t ids_dtype, int32_t n_experts,
+                      int64_t T, int32_t k, int64_t H, void* out, int32_t out_dtype, int64_t s_ot, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BH_HEX_H */

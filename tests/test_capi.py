@@ -1,0 +1,92 @@
+"""The C-ABI library without a GPU: it loads, exports every function include/bh_hex.h declares,
+and rejects bad arguments on the host (status codes and messages) before touching the device."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from blackhole_runtime import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "bh_hex.h"
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(bh_hex_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_bound_functions():
+    assert declared_functions() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.bh_hex_abi_version() == _lib.ABI_VERSION
+    assert lib.bh_hex_last_error() == b""
+
+
+def test_struct_layouts_match_header():
+    # bh_hex_proj: 4 pointers, 4 int64 strides, int32 block (+ padding); bh_hex_tile: 3 int32
+    assert ctypes.sizeof(_lib.HexProj) == 72 and _lib.HexProj.block.offset == 64
+    assert ctypes.sizeof(_lib.HexTile) == 12
+
+
+def test_align_max_blocks_formula():
+    lib = _lib.load()
+    for S, n, bm in ((0, 8, 16), (8, 4, 4), (128, 96, 16), (32768, 96, 64), (5, 100, 16)):
+        assert lib.bh_hex_align_max_blocks(S, n, bm) == -(-S // bm) + min(n, S)
+    assert lib.bh_hex_align_max_blocks(4, 4, 0) == -1
+
+
+def _status(rc, code, pattern):
+    lib = _lib.load()
+    assert rc == code
+    assert re.search(pattern, lib.bh_hex_last_error().decode())
+
+
+def test_host_side_errors():
+    lib = _lib.load()
+    _status(lib.bh_hex_align(None, _lib.I64, 8, 4, 0, None, None, None, None), _lib.ERR_VALUE, "block_m")
+    _status(lib.bh_hex_align(None, _lib.F32, 8, 4, 16, None, None, None, None), _lib.ERR_UNSUPPORTED, "ids dtype")
+    _status(lib.bh_hex_align(None, _lib.I64, 8, 5000, 16, None, None, None, None), _lib.ERR_UNSUPPORTED, "experts")
+    _status(lib.bh_hex_direct(None, _lib.I32, -1, 16, None, None, None, None), _lib.ERR_VALUE, "slot count")
+    _status(lib.bh_hex_route_topk(None, _lib.F32, 8, 2, 8, 9, 1, None, None, _lib.I64, None), _lib.ERR_VALUE, "k must")
+    _status(lib.bh_hex_route_topk(None, _lib.F32, 8, 2, 2000, 8, 1, None, None, _lib.I64, None),
+            _lib.ERR_UNSUPPORTED, "experts")
+    w = _lib.HexProj(16, 16, 16, 16, 0, 0, 0, 0, 32)
+    _status(lib.bh_hex_dequant(ctypes.byref(w), 5, 1, 1, 64, None, 16, _lib.F32, 0, 0, 0, 0, None),
+            _lib.ERR_UNSUPPORTED, "bits")
+    _status(lib.bh_hex_dequant(ctypes.byref(w), 4, 1, 1, 48, None, 16, _lib.F32, 0, 64, 0, 0, None),
+            _lib.ERR_ASSERT, "multiple of 32")
+    bad = _lib.HexProj(16, 16, 16, 16, 0, 0, 0, 0, 48)
+    _status(lib.bh_hex_dequant(ctypes.byref(bad), 4, 1, 1, 96, None, 16, _lib.F32, 0, 96, 0, 0, None),
+            _lib.ERR_VALUE, "scale block")
+    tile = _lib.HexTile(16, 32, 1)
+    _status(lib.bh_hex_moe_glu(16, _lib.BF16, 64, 16, 64, ctypes.byref(w), ctypes.byref(w), 4, 64, 64,
+                               16, 16, 1, 16, 16, 4, 4, 1, ctypes.byref(tile), None),
+            _lib.ERR_UNSUPPORTED, "block_n")
+    tile = _lib.HexTile(16, 64, 1)
+    _status(lib.bh_hex_moe_glu(16, _lib.F32, 64, 16, 64, ctypes.byref(w), ctypes.byref(w), 4, 64, 64,
+                               16, 16, 1, 16, 16, 4, 4, 1, ctypes.byref(tile), None),
+            _lib.ERR_UNSUPPORTED, "BF16 or F16")
+    _status(lib.bh_hex_moe_reduce(16, 6, 16, _lib.I64, 4, 2, 2, 6, 16, _lib.BF16, 6, None),
+            _lib.ERR_UNSUPPORTED, "H % 4")
+
+
+def test_check_maps_status_to_reference_exceptions():
+    lib = _lib.load()
+    lib.bh_hex_align(None, _lib.I64, 8, 4, 0, None, None, None, None)
+    with pytest.raises(ValueError, match="block_m"):
+        _lib.check(_lib.ERR_VALUE, "x")
+    with pytest.raises(AssertionError):
+        _lib.check(_lib.ERR_ASSERT, "x")
+    with pytest.raises(NotImplementedError):
+        _lib.check(_lib.ERR_UNSUPPORTED, "x")
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.ERR_HIP, "x")

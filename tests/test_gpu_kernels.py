@@ -1,0 +1,325 @@
+"""HIP kernels against the CPU oracle on the same seeded inputs (called through the C ABI).
+
+Bit-exact: dequant (each association order, every output dtype, every fp8 code), align, direct,
+routing ids. Tolerance: routing weights (2 ulp), layer outputs (max|got - ref| / max|ref| <= 1e-2
+with bf16/f16 activations, the north-star bound; 1e-4 for float32 activations on the dequant
+path, the reference's own bound at runtime/tests/test_hex_moe.py:81)."""
+
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from blackhole_runtime import hex_moe as hm
+from oracle import hex_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL_16 = 1e-2
+
+
+def say(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def dev_parts(p: dict) -> dict:
+    return {"idx": torch.from_numpy(np.ascontiguousarray(p["idx"]).view(np.int32)).to(DEV),
+            "block_scale": torch.from_numpy(np.ascontiguousarray(p["block_scale"])).to(DEV),
+            "expert_scale": torch.from_numpy(np.ascontiguousarray(p["expert_scale"], np.float32)).to(DEV),
+            "levels": torch.from_numpy(np.ascontiguousarray(p["levels"], np.float32)).to(DEV)}
+
+
+def make_layer(E, H, I, split, bits=(4, 3), seed=0, block=32, quantized=False):
+    """(oracle tiers with numpy parts, prepared HexTiers on the GPU)."""
+    rng = np.random.default_rng(seed)
+    perm = rng.permutation(E)
+    groups = [perm[:split], perm[split:]] if split else [perm]
+    ref, tiers = [], []
+    for j, (ids, b) in enumerate(zip(groups, bits)):
+        n = len(ids)
+        if n == 0:
+            continue
+        parts = {}
+        for q, (proj, (o, i)) in enumerate((("gate_proj", (I, H)), ("up_proj", (I, H)), ("down_proj", (H, I)))):
+            if quantized:
+                W = (np.random.default_rng(seed * 100 + 10 * j + q).standard_normal((n, o, i)) * 0.02).astype(np.float32)
+                parts[proj] = O.quantize_stack(W, 1 << b, block)
+            else:
+                parts[proj] = O.random_parts(n, o, i, b, seed=seed * 100 + 10 * j + q, block=block)
+        ref.append({"bits": b, "experts": ids, **parts})
+        tiers.append(hm.HexTier(b, torch.from_numpy(ids.astype(np.int32)),
+                                *[dev_parts(parts[p]) for p in ("gate_proj", "up_proj", "down_proj")]).prepare(E))
+    return ref, tiers
+
+
+def routing(T, E, k, seed=0, skew=False):
+    rng = np.random.default_rng(seed)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    if skew:
+        p = 1.0 / np.arange(1, E + 1) ** 1.1
+        logits = logits + np.log(p / p.sum())[rng.permutation(E)].astype(np.float32)
+    w, ids = O.route_topk(logits, k)
+    return w, ids
+
+
+# --------------------------------------------------------------------------- dequant
+
+
+@pytest.mark.parametrize("bits", [3, 4])
+@pytest.mark.parametrize("block", [32, 128])
+@pytest.mark.parametrize("order", ["R", "D", "T"])
+def test_dequant_bit_exact(bits, block, order):
+    say(f"dequant bits={bits} block={block} order={order}")
+    p = O.random_parts(3, 40, 256, bits, seed=bits * 7 + block, block=block)
+    # every fp8 code, including subnormals, zero and +-480
+    p["block_scale"] = (np.arange(p["block_scale"].size) % 256).astype(np.uint8).reshape(p["block_scale"].shape)
+    want = O.dequant(p["idx"], p["block_scale"], p["expert_scale"], p["levels"], bits, order)
+    d = dev_parts(p)
+    for dt in (torch.float32, torch.bfloat16, torch.float16):
+        got = hm.hex_dequant(d["idx"], d["block_scale"], d["expert_scale"], d["levels"], bits, order, dt).cpu()
+        exp = torch.from_numpy(want).to(dt)
+        assert torch.equal(got.view(torch.int16 if dt != torch.float32 else torch.int32),
+                           exp.view(torch.int16 if dt != torch.float32 else torch.int32)), dt
+
+
+def test_dequant_all_places_experts():
+    say("dequant_all placement")
+    ref, tiers = make_layer(7, 64, 32, 3, seed=9)
+    w13, w2 = hm.dequant_all(tiers, torch.float32)
+    w13, w2 = w13.cpu().numpy(), w2.cpu().numpy()
+    for t in ref:
+        for local, e in enumerate(t["experts"].tolist()):
+            for proj, got in (("gate_proj", w13[e, :32]), ("up_proj", w13[e, 32:]), ("down_proj", w2[e])):
+                q = t[proj]
+                want = O.dequant(q["idx"][local:local + 1], q["block_scale"][local:local + 1],
+                                 q["expert_scale"][local:local + 1], q["levels"][local:local + 1], t["bits"], "D")[0]
+                assert np.array_equal(got, want), (e, proj)
+
+
+# --------------------------------------------------------------------------- routing and plans
+
+
+@pytest.mark.parametrize("S,n,bm,skew,idt", [(0, 8, 16, False, torch.int64), (1, 96, 16, False, torch.int64),
+                                             (8, 4, 4, False, torch.int32), (37, 5, 4, False, torch.int64),
+                                             (128, 96, 16, False, torch.int64), (512, 96, 16, False, torch.int32),
+                                             (2048, 96, 32, True, torch.int64), (3000, 1000, 16, False, torch.int64),
+                                             (32768, 96, 64, False, torch.int64), (40000, 128, 16, True, torch.int32)])
+def test_align_bit_exact(S, n, bm, skew, idt):
+    say(f"align S={S} n={n} bm={bm} skew={skew} {idt}")
+    rng = np.random.default_rng(S + n + bm)
+    p = None
+    if skew:
+        p = 1.0 / np.arange(1, n + 1) ** 1.1
+        p /= p.sum()
+    ids = rng.choice(n, S, p=p) if S else np.zeros(0, np.int64)
+    want = O.align(ids, n, bm)
+    got = hm.align(torch.from_numpy(ids).to(idt).to(DEV), n, bm)
+    for g, w in zip(got, want):
+        assert np.array_equal(g.cpu().numpy(), w)
+
+
+def test_align_reference_example():
+    say("align reference example")
+    ids = torch.tensor([2, 0, 0, 2, 2, 1, 3, 0], device=DEV)
+    sid, eid, npp = hm.align(ids, 4, 4)
+    assert sid.tolist() == [1, 2, 7, 8, 5, 8, 8, 8, 0, 3, 4, 8, 6, 8, 8, 8] + [8] * 8
+    assert eid.tolist() == [0, 1, 2, 3, -1, -1] and npp.tolist() == [16]
+
+
+@pytest.mark.parametrize("S,bm", [(1, 16), (8, 16), (32, 16), (5, 4)])
+def test_direct_bit_exact(S, bm):
+    say(f"direct S={S} bm={bm}")
+    ids = np.random.default_rng(S).integers(0, 96, S)
+    got = hm.direct(torch.from_numpy(ids).to(DEV), bm)
+    for g, w in zip(got, O.direct(ids, bm)):
+        assert np.array_equal(g.cpu().numpy(), w)
+
+
+@pytest.mark.parametrize("T,E,k,dt", [(1, 8, 2, torch.float32), (16, 96, 8, torch.float32),
+                                      (300, 128, 8, torch.bfloat16), (7, 1000, 4, torch.float32),
+                                      (4, 7, 7, torch.float16)])
+def test_route_topk(T, E, k, dt):
+    say(f"route_topk T={T} E={E} k={k} {dt}")
+    g = torch.Generator().manual_seed(T + E)
+    logits = torch.randn(T, E, generator=g).to(dt)
+    w_ref, i_ref = O.route_topk(logits.float().numpy(), k)
+    w, ids = hm.route_topk(logits.to(DEV), k)
+    assert np.array_equal(ids.cpu().numpy(), i_ref)
+    np.testing.assert_allclose(w.cpu().numpy(), w_ref, rtol=5e-7, atol=0)
+    w2, ids2 = hm.route_topk(logits.to(DEV), k, renormalize=False, ids_dtype=torch.int32)
+    assert np.array_equal(ids2.cpu().numpy(), i_ref)
+    p = torch.softmax(logits.float(), -1).gather(1, torch.from_numpy(i_ref)).numpy()
+    np.testing.assert_allclose(w2.cpu().numpy(), p, rtol=5e-7, atol=1e-12)
+
+
+# --------------------------------------------------------------------------- the fused layer
+
+
+def run_fused(ref, tiers, T, E, k, H, dt=torch.bfloat16, seed=1, config=None, align_mode="auto", skew=False,
+              path="fused"):
+    w, ids = routing(T, E, k, seed=seed, skew=skew)
+    x = torch.from_numpy(np.random.default_rng(seed + 1).standard_normal((T, H)).astype(np.float32)).to(dt)
+    act_round = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: None}[dt]
+    want = O.moe_reference(x.float().numpy(), w, ids, ref, act_round)
+    xd, wd, idd = x.to(DEV), torch.from_numpy(w).to(DEV), torch.from_numpy(ids).to(DEV)
+    if path == "fused":
+        got = hm.hex_moe_fused(xd, wd, idd, tiers, config, align_mode)
+    else:
+        got = hm.hex_moe(xd, wd, idd, tiers, config, path)
+    assert got.dtype == dt and got.shape == (T, H)
+    return O.rel_err(got.float().cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("T,split,bits", [(1, 0, (3,)), (3, 5, (4, 3)), (40, 4, (4, 3)), (4, 0, (4,)),
+                                          (16, 6, (4, 3)), (64, 0, (4,))])
+def test_reference_suite_shapes(T, split, bits):
+    """runtime/tests/test_hex_moe.py:64-81's shapes (E=12, H=128, I=64, k=4) in bf16 through the
+    fused kernels with both plans; float32 through the dequant path at the reference's 1e-4."""
+    say(f"reference shapes T={T} split={split} bits={bits}")
+    E, H, I, k = 12, 128, 64, 4
+    ref, tiers = make_layer(E, H, I, split, bits, seed=T)
+    for mode in ("auto", "direct", "torch"):
+        err = run_fused(ref, tiers, T, E, k, H, seed=T, align_mode=mode)
+        assert err < TOL_16, (mode, err)
+    small = {"BLOCK_M": 16, "BLOCK_N": 32, "BLOCK_K": 32, "num_warps": 4, "num_stages": 1}
+    assert run_fused(ref, tiers, T, E, k, H, seed=T, config=small) < TOL_16
+    assert run_fused(ref, tiers, T, E, k, H, dt=torch.float32, seed=T, path="dequant") < 1e-4
+    assert run_fused(ref, tiers, T, E, k, H, dt=torch.float32, seed=T, path="auto") < 1e-4
+
+
+@pytest.mark.parametrize("bm", [16, 32, 64])
+@pytest.mark.parametrize("ks", [1, 2, 4])
+@pytest.mark.parametrize("block", [32, 128])
+def test_tiles(bm, ks, block):
+    say(f"tiles bm={bm} ks={ks} block={block}")
+    E, H, I, k = 16, 256, 128, 4
+    ref, tiers = make_layer(E, H, I, 8, (4, 3), seed=bm + ks, block=block)
+    cfg = {"BLOCK_M": bm, "BLOCK_N": 64 // ks}
+    for T in (1, 24, 70):
+        err = run_fused(ref, tiers, T, E, k, H, seed=T, config=cfg)
+        assert err < TOL_16, (T, err)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("bits", [3, 4])
+def test_quantized_layer(dt, bits):
+    """Weights from the HEX quantizer (N(0, 0.02)), as the benchmark configs are built."""
+    say(f"quantized layer {dt} bits={bits}")
+    E, H, I, k = 8, 256, 128, 2
+    ref, tiers = make_layer(E, H, I, 0, (bits,), seed=3, quantized=True)
+    for T in (1, 16):
+        assert run_fused(ref, tiers, T, E, k, H, dt=dt, seed=T) < TOL_16
+
+
+def test_skewed_routing_and_odd_widths():
+    """Zipf-skewed routing (hot experts over several blocks); widths 160 and 96, not multiples of
+    the 128-input step or the 64-row tile."""
+    say("skewed routing, odd widths")
+    E, H, I, k = 10, 160, 96, 3
+    ref, tiers = make_layer(E, H, I, 5, (4, 3), seed=21)
+    for T, cfg in ((200, None), (200, {"BLOCK_M": 64, "BLOCK_N": 16}), (33, {"BLOCK_M": 32, "BLOCK_N": 32})):
+        assert run_fused(ref, tiers, T, E, k, H, seed=T, config=cfg, skew=True) < TOL_16
+
+
+def test_fp8_special_codes_in_fused_path():
+    """Scale codes 0x7F / 0xFF decode to +-480 (the reference formula) in the fused kernels too."""
+    say("fp8 0x7F in fused path")
+    E, H, I, k = 4, 128, 64, 2
+    ref, tiers = make_layer(E, H, I, 0, (4,), seed=5)
+    for t_ref, t in zip(ref, tiers):
+        for proj in ("gate_proj", "up_proj", "down_proj"):
+            bs = t_ref[proj]["block_scale"]
+            bs.reshape(-1)[::7] = 0x7F
+            bs.reshape(-1)[3::11] = 0xFF
+            getattr(t, proj)["block_scale"].copy_(torch.from_numpy(bs))
+    assert run_fused(ref, tiers, 3, E, k, H, seed=2) < TOL_16
+
+
+def _exact_layer(E, H, I, bits):
+    """Parts whose dequantized weights, activations and all partial sums are exact in float32:
+    levels k/8, power-of-two block scales, unit expert scales."""
+    rng = np.random.default_rng(bits)
+    L = 1 << bits
+    parts = {}
+    for proj, (o, i) in (("gate_proj", (I, H)), ("up_proj", (I, H)), ("down_proj", (H, I))):
+        parts[proj] = {"idx": O.pack(rng.integers(0, L, (E, o, i)), bits),
+                       "block_scale": rng.choice(np.array([0x30, 0x38, 0x40], np.uint8), (E, o, i // 32)),
+                       "expert_scale": np.ones(E, np.float32),
+                       "levels": ((np.arange(L) - L // 2) / 8.0).astype(np.float32)[None].repeat(E, 0)}
+    return parts
+
+
+@pytest.mark.parametrize("bits", [3, 4])
+def test_down_kernel_exact(bits):
+    """With exactly representable operands the down kernel's y must equal the float64 sum bit
+    for bit: pins the code -> input mapping, the block -> scale mapping and the slot rows."""
+    say(f"down exact bits={bits}")
+    E, H, I, k, T = 6, 64, 128, 2, 5
+    parts = _exact_layer(E, H, I, bits)
+    tier = hm.HexTier(bits, torch.arange(E, dtype=torch.int32),
+                      *[dev_parts(parts[p]) for p in ("gate_proj", "up_proj", "down_proj")]).prepare(E)
+    rng = np.random.default_rng(7)
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)])
+    S = T * k
+    act = rng.integers(-4, 5, (S, I)).astype(np.float32)
+    tw = np.full(S, 0.5, np.float32)
+    Wd = O.dequant(parts["down_proj"]["idx"], parts["down_proj"]["block_scale"], parts["down_proj"]["expert_scale"],
+                   parts["down_proj"]["levels"], bits, "R").astype(np.float64)
+    want = np.stack([Wd[ids.reshape(-1)[s]] @ act[s].astype(np.float64) * 0.5 for s in range(S)])
+    for bm, ks in ((16, 1), (32, 2), (16, 4)):
+        sid, eid, npp = hm.plan(torch.from_numpy(ids).to(DEV).reshape(-1), E, bm, "torch")
+        y = torch.full((S, H), float("nan"), device=DEV)
+        hm._launch_down(torch.from_numpy(act).to(torch.bfloat16).to(DEV), y, tier, sid, eid, npp, S,
+                        torch.from_numpy(tw).to(DEV), bm, ks)
+        assert np.array_equal(y.cpu().numpy(), want.astype(np.float32)), (bm, ks)
+
+
+def test_uncovered_experts_contribute_nothing():
+    say("uncovered experts")
+    E, H, I, k = 8, 64, 32, 2
+    ref, tiers = make_layer(E, H, I, 3, (4, 3), seed=4)
+    ref, tiers = ref[:1], tiers[:1]          # experts of the second tier have no weights
+    assert run_fused(ref, tiers, 9, E, k, H, seed=3) < TOL_16
+
+
+def test_width_mismatch_and_dtype_errors():
+    say("errors")
+    E, H, I, k = 4, 64, 32, 2
+    _, tiers = make_layer(E, H, I, 0, (4,), seed=1)
+    x = torch.zeros(2, 96, dtype=torch.bfloat16, device=DEV)
+    w = torch.full((2, k), 0.5, device=DEV)
+    ids = torch.zeros(2, k, dtype=torch.long, device=DEV)
+    with pytest.raises(AssertionError, match="input width"):
+        hm.hex_moe_fused(x, w, ids, tiers)
+    with pytest.raises(NotImplementedError, match="bf16 or f16"):
+        hm.hex_moe_fused(torch.zeros(2, H, device=DEV), w, ids, tiers)
+
+
+def test_graph_capture_replays_match_eager():
+    """The fused path captured in a hipGraph: several replays, with eager work between them,
+    each equal to the eager result."""
+    say("graph capture")
+    E, H, I, k, T = 16, 256, 128, 4, 8
+    ref, tiers = make_layer(E, H, I, 8, (4, 3), seed=12)
+    w, ids = routing(T, E, k, seed=5)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(0)).to(torch.bfloat16).to(DEV)
+    wd, idd = torch.from_numpy(w).to(DEV), torch.from_numpy(ids).to(DEV)
+    eager = hm.hex_moe_fused(x, wd, idd, tiers)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        hm.hex_moe_fused(x, wd, idd, tiers)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = hm.hex_moe_fused(x, wd, idd, tiers)
+    for i in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), i
+        _ = hm.hex_moe_fused(x * 2, wd, idd, tiers)      # unrelated eager work between replays
+        torch.cuda.synchronize()

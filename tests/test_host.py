@@ -1,0 +1,262 @@
+"""Host logic without a GPU: tile choice, HexTier.prepare, the GPU-only guard, and the
+"blackhole-hex" vLLM plugin against fake vLLM modules (as runtime/tests/test_folder.py:60-93
+tests the reference's plugin)."""
+
+from __future__ import annotations
+
+import sys
+import types
+
+import numpy as np
+import pytest
+import torch
+
+from blackhole_runtime import hex_moe as hm
+from blackhole_runtime import vllm_hex
+from oracle import hex_oracle as O
+
+
+def _parts(n, out, inp, bits, seed):
+    p = O.random_parts(n, out, inp, bits, seed=seed)
+    return {"idx": torch.from_numpy(p["idx"].view(np.int32)).view(torch.uint32) if hasattr(torch, "uint32")
+            else torch.from_numpy(p["idx"].view(np.int32)),
+            "block_scale": torch.from_numpy(p["block_scale"]), "expert_scale": torch.from_numpy(p["expert_scale"]),
+            "levels": torch.from_numpy(p["levels"])}
+
+
+def _tier(ids, bits, H=64, I=32, seed=0):
+    n = len(ids)
+    return hm.HexTier(bits, torch.tensor(ids), _parts(n, I, H, bits, seed + 1), _parts(n, I, H, bits, seed + 2),
+                      _parts(n, H, I, bits, seed + 3))
+
+
+def test_prepare_views_lookup_and_structs():
+    t = _tier([3, 0, 5], 4).prepare(6)
+    assert t.gate_proj["idx"].dtype == torch.int32 and t.experts.dtype == torch.int32
+    assert t.lookup.tolist() == [1, -1, -1, 0, -1, 2]
+    s = t.struct("down_proj")
+    assert s.block == 32 and s.s_in == t.down_proj["idx"].stride(1)
+    with pytest.raises(ValueError, match="expert ids"):
+        _tier([0, 7], 4).prepare(6)
+    with pytest.raises(ValueError, match="levels"):
+        _tier([0], 3).__class__(4, torch.tensor([0]), *[_parts(1, 8, 64, 3, 1)] * 3).prepare(2)
+
+
+def test_block_from_shapes_128():
+    t = _tier([0], 4, H=256, I=128)
+    for name in ("gate_proj", "up_proj", "down_proj"):
+        p = getattr(t, name)
+        p["block_scale"] = p["block_scale"][..., ::4].contiguous()
+    t.prepare(1)
+    assert t.struct("gate_proj").block == 128 and t.struct("down_proj").block == 128
+
+
+def test_default_config_and_env(monkeypatch):
+    c = hm.default_config(8, 768, 2048, True, 96)          # T=1 decode: 8 expert blocks
+    assert c["BLOCK_M"] == 16 and c["K_SPLIT"] == 4
+    c = hm.default_config(128, 768, 2048, True, 96)        # T=16
+    assert c["BLOCK_M"] == 16 and c["K_SPLIT"] in (1, 2)
+    c = hm.default_config(32768, 2048, 768, False, 96)     # prefill: many slots per expert
+    assert c["BLOCK_M"] == 64
+    assert hm.default_config(32768, 768, 2048, True, 96)["BLOCK_M"] == 32
+    monkeypatch.setenv("BLACKHOLE_HEX_TILES", "32,32")
+    assert hm.default_config(8, 768, 2048, True, 96) == {"BLOCK_M": 32, "BLOCK_N": 32, "K_SPLIT": 2}
+    # the reference's own config keys map onto the tile
+    assert hm._tile_from({"BLOCK_M": 16, "BLOCK_N": 32, "BLOCK_K": 32, "num_warps": 4, "num_stages": 1}) == (16, 2)
+    assert hm._tile_from({"BLOCK_M": 128, "BLOCK_N": 128}) == (64, 1)
+
+
+def test_kernels_refuse_cpu_tensors():
+    x = torch.zeros(2, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU"):
+        hm.align(torch.zeros(4, dtype=torch.long), 4, 16)
+    t = _tier([0, 1], 4).prepare(2)
+    with pytest.raises(ValueError, match="GPU"):
+        hm.hex_moe_fused(x, torch.ones(2, 1), torch.zeros(2, 1, dtype=torch.long), [t])
+    with pytest.raises(ValueError, match="unknown path"):
+        hm.hex_moe(x, torch.ones(2, 1), torch.zeros(2, 1, dtype=torch.long), [t], path="triton")
+
+
+# --------------------------------------------------------------------------- the vLLM plugin
+
+
+def test_tier_param_names():
+    assert vllm_hex.tier_param_name("model.layers.0.mlp.experts.tier16.experts") == "hex_t16_experts"
+    assert vllm_hex.tier_param_name("tier8.down_proj.levels") == "hex_t8_down_proj_levels"
+    with pytest.raises(ValueError, match="unexpected expert tensor"):
+        vllm_hex.tier_param_name("experts.0.gate_proj.weight", "layer")
+
+
+def _params(tiers):
+    out = {}
+    for L, t in tiers:
+        out[f"hex_t{L}_experts"] = t.experts
+        for proj in ("gate_proj", "up_proj", "down_proj"):
+            for q in ("idx", "block_scale", "expert_scale", "levels"):
+                out[f"hex_t{L}_{proj}_{q}"] = getattr(t, proj)[q]
+    return out
+
+
+def test_assemble_tiers_checks():
+    good = [(16, _tier([0, 2], 4)), (8, _tier([1, 3], 3, seed=5))]
+    tiers = vllm_hex.assemble_tiers(_params(good), (4, 64, 32), "l0")
+    assert [t.bits for t in tiers] == [4, 3]
+    with pytest.raises(ValueError, match=r"no weights for experts \[3\]"):
+        vllm_hex.assemble_tiers(_params([(16, _tier([0, 2], 4)), (8, _tier([1], 3))]), (4, 64, 32), "l0")
+    with pytest.raises(ValueError, match="shapes do not match"):
+        vllm_hex.assemble_tiers(_params(good), (4, 64, 48), "l0")
+    with pytest.raises(ValueError, match="no HEX experts"):
+        vllm_hex.assemble_tiers({}, (4, 64, 32), "l0")
+
+
+def _fake_vllm(monkeypatch):
+    registry = {}
+
+    def mod(name):
+        m = types.ModuleType(name)
+        monkeypatch.setitem(sys.modules, name, m)
+        return m
+
+    for name in ("vllm", "vllm.model_executor", "vllm.model_executor.layers"):
+        mod(name)
+    fm = mod("vllm.model_executor.layers.fused_moe")
+
+    class FusedMoEMethodBase:
+        def __init__(self, moe):
+            self.moe = moe
+
+    class RoutedExperts:
+        pass
+
+    fm.FusedMoEMethodBase, fm.RoutedExperts = FusedMoEMethodBase, RoutedExperts
+    lin = mod("vllm.model_executor.layers.linear")
+
+    class LinearBase:
+        pass
+
+    class UnquantizedLinearMethod:
+        pass
+
+    lin.LinearBase, lin.UnquantizedLinearMethod = LinearBase, UnquantizedLinearMethod
+    q = mod("vllm.model_executor.layers.quantization")
+
+    def register_quantization_config(name):
+        def deco(cls):
+            registry[name] = cls
+            return cls
+        return deco
+
+    q.register_quantization_config = register_quantization_config
+    bc = mod("vllm.model_executor.layers.quantization.base_config")
+
+    class QuantizationConfig:
+        pass
+
+    bc.QuantizationConfig = QuantizationConfig
+    ve = mod("vllm.model_executor.layers.vocab_parallel_embedding")
+
+    class UnquantizedEmbeddingMethod:
+        def process_weights_after_loading(self, layer):
+            pass
+
+        def apply(self, layer, x, bias=None):
+            return x @ layer.weight.T
+
+    class ParallelLMHead:
+        pass
+
+    ve.ParallelLMHead, ve.UnquantizedEmbeddingMethod = ParallelLMHead, UnquantizedEmbeddingMethod
+    return registry, RoutedExperts, ParallelLMHead, LinearBase
+
+
+def test_register_with_fake_vllm(monkeypatch):
+    registry, RoutedExperts, ParallelLMHead, LinearBase = _fake_vllm(monkeypatch)
+    vllm_hex.register()
+    vllm_hex.register()                                       # idempotent
+    cfg = registry[vllm_hex.NAME].from_config({"quant_method": "blackhole-hex", "head_ids": [1, 3]})
+    assert cfg.get_name() == "blackhole-hex" and cfg.get_min_capability() == 80
+    assert cfg.get_supported_act_dtypes() == [torch.bfloat16, torch.float16]
+
+    class Layer(RoutedExperts, torch.nn.Module):
+        def __init__(self):
+            torch.nn.Module.__init__(self)
+            self.moe_config = types.SimpleNamespace(tp_size=1, ep_size=1)
+            self.layer_name = "model.layers.0.mlp.experts"
+
+    layer = Layer()
+    method = cfg.get_quant_method(layer, "p")
+    assert type(method).__name__ == "HexMoEMethod"
+    method.create_weights(layer, 4, 64, 32, torch.bfloat16)
+    src = [(16, _tier([0, 2], 4)), (8, _tier([1, 3], 3, seed=5))]
+    weights = []
+    for L, t in src:
+        weights.append((f"tier{L}.experts", t.experts))
+        for proj in ("gate_proj", "up_proj", "down_proj"):
+            for part in ("idx", "block_scale", "expert_scale", "levels"):
+                weights.append((f"tier{L}.{proj}.{part}", getattr(t, proj)[part]))
+    loaded = list(layer.load_weights(iter(weights)))
+    assert "hex_t16_gate_proj_idx" in loaded and len(loaded) == len(weights)
+    method.process_weights_after_loading(layer)
+    assert [t.bits for t in layer.hex_tiers] == [4, 3]
+    with pytest.raises(ValueError, match="unexpected expert tensor"):
+        list(layer.load_weights(iter([("experts.0.w1", torch.zeros(1))])))
+    bad = Layer()
+    bad.moe_config = types.SimpleNamespace(tp_size=2, ep_size=1)
+    with pytest.raises(ValueError, match="one GPU"):
+        cfg.get_quant_method(bad, "p").create_weights(bad, 4, 64, 32, torch.bfloat16)
+
+    class Head(ParallelLMHead, torch.nn.Module):
+        def __init__(self):
+            torch.nn.Module.__init__(self)
+            self.weight = torch.nn.Parameter(torch.ones(5, 3), requires_grad=False)
+
+    head = Head()
+    hm_ = cfg.get_quant_method(head, "lm_head")
+    hm_.process_weights_after_loading(head)
+    logits = hm_.apply(head, torch.ones(2, 3))
+    assert logits[0].tolist() == [vllm_hex.HEAD_FILL + 3, 3.0, vllm_hex.HEAD_FILL + 3, 3.0, vllm_hex.HEAD_FILL + 3]
+
+    class Lin(LinearBase):
+        pass
+
+    assert type(cfg.get_quant_method(Lin(), "q")).__name__ == "UnquantizedLinearMethod"
+    assert cfg.get_quant_method(object(), "x") is None
+
+
+def test_qwen4_exp_ple_embedding_patch(monkeypatch):
+    """The counterpart of runtime/tests/test_folder.py:60-93."""
+    calls = []
+
+    class Method:
+        @staticmethod
+        def from_quant_config(quant_config, prefix, embedding_dtype=None):
+            calls.append(quant_config)
+            if quant_config is not None and quant_config.get_name() != "fp8":
+                raise NotImplementedError("unsupported")
+            return "plain" if quant_config is None else "fp8"
+
+    ng = types.ModuleType("vllm.models.qwen4_exp.common.ngram_embedding")
+    ng.Qwen4ExpPLEEmbeddingMethod = Method
+    for name in ("vllm", "vllm.models", "vllm.models.qwen4_exp", "vllm.models.qwen4_exp.common"):
+        monkeypatch.setitem(sys.modules, name, types.ModuleType(name))
+    sys.modules["vllm.models.qwen4_exp.common"].ngram_embedding = ng
+    monkeypatch.setitem(sys.modules, ng.__name__, ng)
+
+    class Q:
+        def __init__(self, n):
+            self.n = n
+
+        def get_name(self):
+            return self.n
+
+    assert vllm_hex.plain_ple_embedding() and vllm_hex.plain_ple_embedding()
+    assert Method.from_quant_config(Q(vllm_hex.NAME), "model.layers.1.ple") == "plain"
+    assert Method.from_quant_config(Q("online"), "model.layers.1.ple") == "plain"
+    assert Method.from_quant_config(Q("fp8"), "x") == "fp8"
+    with pytest.raises(NotImplementedError):
+        Method.from_quant_config(Q("awq"), "x")
+
+
+def test_plain_ple_embedding_without_vllm(monkeypatch):
+    monkeypatch.setitem(sys.modules, "vllm", None)
+    assert vllm_hex.plain_ple_embedding() is False
