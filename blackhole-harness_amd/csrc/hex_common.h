@@ -39,7 +39,10 @@ __device__ __forceinline__ uint32_t bf16_bits(float f) {
 __device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 
 // float -> fp16 bits, round to nearest even (the conversion instruction rounds to nearest even).
+// The empty asm keeps the compiler from folding a preceding multiply into the conversion as
+// v_fma_mixlo_f16 a, b, 0: adding +0 turns a -0 product into +0.
 __device__ __forceinline__ uint32_t f16_bits(float f) {
+  asm volatile("" : "+v"(f));
   _Float16 h = (_Float16)f;
   return (uint32_t)__builtin_bit_cast(uint16_t, h);
 }

@@ -187,7 +187,7 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(const void* __rest
   while ((1 << nbits) <= n) ++nbits;          // ids in [0, n] (n marks "not placed")
   const uint64_t below = (lane ? (~0ull >> (64 - lane)) : 0ull);
   for (int64_t c0 = 0; c0 < S; c0 += kAlignThreads) {
-    for (int i = tid; i < kAlignWaves * n; i += kAlignThreads) (&wcnt[0][0])[i] = 0;
+    for (int i = tid; i < kAlignWaves * n; i += kAlignThreads) wcnt[i / n][i % n] = 0;
     const int64_t i = c0 + tid;
     int key = n;
     if (i < S) {
@@ -214,7 +214,10 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(const void* __rest
       cnt[e] = acc;
     }
     __syncthreads();
-    if (key < n) sorted_ids[start[key] + wcnt[w][key] + rank] = (int32_t)i;
+    if (key < n) {
+      const int64_t pos = (int64_t)start[key] + wcnt[w][key] + rank;
+      if (pos < max_blocks * bm) sorted_ids[pos] = (int32_t)i;
+    }
     __syncthreads();
   }
 }
