@@ -1,0 +1,378 @@
+"""HEX MoE layer benchmark on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 400] [--warmup 40] [--config 2] [--tokens 16]
+                    [--no-sweep] [--no-cpu-baseline]
+
+A step is one HEX MoE layer call (hex_moe through the fused HIP kernels: slot plan, gate/up +
+SiLU, down + top-k weight, k-slot sum) on one batch of synthetic tokens with inputs resident
+in HBM. Eight copies of the layer's weights stay resident and the steps cycle through them, so
+weights stream from HBM rather than the 256 MB Infinity Cache; the eight calls are captured in
+one hipGraph (as a serving engine captures its layers) and replayed. The timed region is
+bracketed by torch.cuda.synchronize(); one JSON line goes to stdout, progress to stderr.
+
+Synthetic data (no checkpoints): weights N(0, 0.02) quantized to HEX on the GPU (16 levels
+rounded to fp16 for 4-bit, 8 for 3-bit; fp8 scale per 128 inputs), activations bf16 N(0, 1),
+router logits N(0, 1) through the softmax top-k routing kernel. Seeds: weights 0, activations 1,
+logits 2, REAQ tiering 3.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "blackhole-harness_amd"))
+
+CONFIGS = {
+    1: dict(name="config1 tiny: E=8 H=256 I=128 top-2, HEX 4-bit", E=8, H=256, I=128, k=2, bits=4, T=16),
+    2: dict(name="config2 decode: Qwen3-30B-A3B after 25% REAP, E=96 H=2048 I=768 top-8, HEX 4-bit",
+            E=96, H=2048, I=768, k=8, bits=4, T=16),
+    3: dict(name="config3 prefill: E=96 H=2048 I=768 top-8, HEX 3-bit (3.25 bpw)", E=96, H=2048, I=768, k=8,
+            bits=3, T=4096),
+    4: dict(name="config4 REAQ: 48x4-bit + 48x3-bit, Zipf(1.1) routing", E=96, H=2048, I=768, k=8, bits=4,
+            T=256, reaq=48, zipf=1.1),
+    5: dict(name="config5: Qwen3-235B-A22B shape, E=128 H=4096 I=1536 top-8, HEX 4-bit", E=128, H=4096, I=1536,
+            k=8, bits=4, T=16),
+}
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def proj_bytes(out: int, inp: int, bits: int, block: int) -> int:
+    """HBM bytes of one expert projection: idx + block scales + expert scale + levels."""
+    return out * inp * bits // 8 + out * inp // block + 4 + 4 * (1 << bits)
+
+
+def build_tiers(cfg, block, copies, dev):
+    """`copies` independent copies of one layer's HexTiers (weights quantized once on the GPU)."""
+    import torch
+
+    from blackhole_runtime import hex_moe as hm
+    from blackhole_runtime import quant
+    E, H, I = cfg["E"], cfg["H"], cfg["I"]
+    g = torch.Generator(device=dev).manual_seed(0)
+    if cfg.get("reaq"):
+        score = torch.rand(E, generator=torch.Generator().manual_seed(3))
+        order = torch.argsort(score, descending=True)
+        groups = [(order[:cfg["reaq"]], 4), (order[cfg["reaq"]:], 3)]
+    else:
+        groups = [(torch.arange(E), cfg["bits"])]
+    base = []
+    for ids, bits in groups:
+        parts = {}
+        for proj, (o, i) in (("gate_proj", (I, H)), ("up_proj", (I, H)), ("down_proj", (H, I))):
+            chunks = []
+            for c0 in range(0, len(ids), 16):
+                n = min(16, len(ids) - c0)
+                W = torch.randn(n, o, i, generator=g, device=dev) * 0.02
+                chunks.append(quant.quantize_experts(W, 1 << bits, block))
+                del W
+            p = {q: torch.cat([c[q] for c in chunks]) for q in chunks[0]}
+            if bits == 4:
+                p["levels"] = p["levels"].half().float()       # 16-level fp16 tables
+            parts[proj] = p
+        base.append((ids.to(torch.int32), bits, parts))
+    out = []
+    for c in range(copies):
+        tiers = []
+        for ids, bits, parts in base:
+            cp = {proj: {q: (t if c == 0 else t.clone()) for q, t in p.items()} for proj, p in parts.items()}
+            tiers.append(hm.HexTier(bits, ids.clone(), cp["gate_proj"], cp["up_proj"], cp["down_proj"]).prepare(E))
+        out.append(tiers)
+    torch.cuda.synchronize()
+    return out
+
+
+def make_inputs(cfg, T, dev):
+    import numpy as np
+    import torch
+
+    from blackhole_runtime import hex_moe as hm
+    E, H, k = cfg["E"], cfg["H"], cfg["k"]
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).to(dev)
+    logits = torch.randn(T, E, generator=torch.Generator().manual_seed(2))
+    if cfg.get("zipf"):
+        p = 1.0 / np.arange(1, E + 1) ** cfg["zipf"]
+        perm = np.random.default_rng(2).permutation(E)
+        logits = logits + torch.from_numpy(np.log(p / p.sum())[perm]).float()
+    w, ids = hm.route_topk(logits.to(dev), k)
+    return x, w, ids, logits
+
+
+def layer_bytes(cfg, tiers, ids, block, T):
+    """(whole-layer algorithmic HBM bytes, gate/up-launch bytes) for the routed experts."""
+    import torch
+    H, I, k = cfg["H"], cfg["I"], cfg["k"]
+    used = set(torch.unique(ids).tolist())
+    total, glu = 0, 0
+    for t in tiers:
+        mine = used.intersection(t._experts_host.tolist())
+        gu = 2 * proj_bytes(I, H, t.bits, block)
+        total += len(mine) * (gu + proj_bytes(H, I, t.bits, block))
+        glu += len(mine) * gu
+    total += 2 * T * H + 2 * T * H + 8 * T * k
+    glu += 2 * T * H + 2 * T * k * I
+    return total, glu, len(used)
+
+
+def graph_of(fn):
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def event_time_ms(g, reps: int) -> float:
+    """Average milliseconds per replay of graph g, from HIP events on the current stream."""
+    import torch
+    g.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        g.replay()
+    b.record()
+    b.synchronize()
+    return a.elapsed_time(b) / reps
+
+
+def kernel_breakdown(cfg, copies, x, w, ids, reps):
+    """Average microseconds per launch of each kernel (graphs of one kernel kind over the copies)."""
+    import torch
+
+    from blackhole_runtime import hex_moe as hm
+    T, k = ids.shape
+    S = T * k
+    E, H, I = cfg["E"], cfg["H"], cfg["I"]
+    flat = ids.reshape(-1)
+    c1 = hm.default_config(S, I, H, True, E)
+    c2 = hm.default_config(S, H, I, False, E)
+    bm1, ks1 = hm._tile_from(c1)
+    bm2, ks2 = hm._tile_from(c2)
+    p1 = hm.plan(flat, E, bm1)
+    p2 = hm.plan(flat, E, bm2)
+    act = torch.empty(S, I, dtype=x.dtype, device=x.device)
+    y = torch.empty(S, H, dtype=torch.float32, device=x.device)
+    wf = w.reshape(-1).float().contiguous()
+    n_tiers = len(copies[0])
+    res = {}
+
+    def glu():
+        for tiers in copies:
+            for t in tiers:
+                hm._launch_glu(x, act, t, *p1, S, k, bm1, ks1)
+
+    def down():
+        for tiers in copies:
+            for t in tiers:
+                hm._launch_down(act, y, t, *p2, S, wf, bm2, ks2)
+
+    def plan():
+        for _ in copies:
+            hm.plan(flat, E, bm1)
+
+    n = len(copies)
+    res["glu_us"] = event_time_ms(graph_of(glu), reps) * 1e3 / (n * n_tiers)
+    res["down_us"] = event_time_ms(graph_of(down), reps) * 1e3 / (n * n_tiers)
+    res["plan_us"] = event_time_ms(graph_of(plan), reps) * 1e3 / n
+    res["tiles"] = {"glu": c1, "down": c2, "plan": "direct" if S <= hm.DIRECT_MAX else "align"}
+    return res
+
+
+def run_layer(cfg, copies, T, steps, warmup, block, breakdown=True):
+    """Time `steps` layer calls (graph replays of len(copies) calls each)."""
+    import torch
+
+    from blackhole_runtime import hex_moe as hm
+    dev = copies[0][0].lookup.device
+    x, w, ids, logits = make_inputs(cfg, T, dev)
+    n = len(copies)
+
+    def layers():
+        for tiers in copies:
+            hm.hex_moe(x, w, ids, tiers, path="fused")
+
+    g = graph_of(layers)
+    reps = max(1, -(-steps // n))
+    for _ in range(max(1, -(-warmup // n))):
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        g.replay()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    calls = reps * n
+    ms = elapsed * 1e3 / calls
+    total, glu_b, used = layer_bytes(cfg, copies[0], ids, block, T)
+    S = T * cfg["k"]
+    flops = 6.0 * S * cfg["H"] * cfg["I"]
+    out = {"T": T, "steps": calls, "ms_per_step": ms, "tokens_per_s": T / (ms * 1e-3), "unique_experts": used,
+           "layer_bytes": total, "hbm_gbps": total / (ms * 1e-3) / 1e9,
+           "hbm_frac": total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+           "mfma_frac": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, "glu_bytes": glu_b}
+    if breakdown:
+        out["kernels"] = kernel_breakdown(cfg, copies, x, w, ids, max(5, reps // 2))
+    return out, (x, w, ids, logits)
+
+
+def cpu_baseline(cfg, tiers, x, w, ids, runs=3):
+    """The CPU oracle (numpy float32 restatement of hex_ref.moe_reference) on one layer call of
+    the same workload, one BLAS thread; median of `runs` calls."""
+    import numpy as np
+
+    from oracle import hex_oracle as O
+    try:
+        from threadpoolctl import threadpool_limits
+    except ImportError:                                  # pragma: no cover
+        threadpool_limits = None
+    ref = []
+    for t in tiers:
+        parts = {}
+        for proj in ("gate_proj", "up_proj", "down_proj"):
+            p = getattr(t, proj)
+            parts[proj] = {"idx": p["idx"].cpu().numpy().view(np.uint32), "block_scale": p["block_scale"].cpu().numpy(),
+                           "expert_scale": p["expert_scale"].cpu().numpy(), "levels": p["levels"].cpu().numpy()}
+        ref.append({"bits": t.bits, "experts": t._experts_host.numpy(), **parts})
+    xn, wn, idn = x.float().cpu().numpy(), w.cpu().numpy(), ids.cpu().numpy()
+    times = []
+    ctx = threadpool_limits(1) if threadpool_limits else None
+    try:
+        if ctx:
+            ctx.__enter__()
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            O.moe_reference(xn, wn, idn, ref, "bf16")
+            times.append(time.perf_counter() - t0)
+            log(f"  cpu baseline call: {times[-1]:.2f} s")
+    finally:
+        if ctx:
+            ctx.__exit__(None, None, None)
+    med = float(np.median(times))
+    model = "unknown CPU"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    T = ids.shape[0]
+    return {"value": T / med, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{runs} calls of the oracle moe_reference (numpy float32, 1 BLAS thread) on the benchmark "
+                      f"layer at T={T}, median {med:.2f} s per call, on {model}"}
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
+    ap.add_argument("--tokens", type=int, default=0, help="token batch (default: the config's)")
+    ap.add_argument("--block", type=int, default=128, help="inputs per fp8 block scale (32 or 128)")
+    ap.add_argument("--copies", type=int, default=8, help="resident layer copies the steps cycle through")
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a 256 MiB device-to-device copy (the known-size kernel that scales "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE into bytes)")
+    a = ap.parse_args(argv)
+    if a.gpus != 1:
+        print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for --gpus {a.gpus})",
+              file=sys.stderr)
+        return 2
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda", 0)
+    cfg = CONFIGS[a.config]
+    T = a.tokens or cfg["T"]
+    log(f"bench: {torch.cuda.get_device_name(dev)}; {cfg['name']}, T={T}, block {a.block}, {a.copies} copies")
+    t0 = time.perf_counter()
+    copies = build_tiers(cfg, a.block, a.copies, dev)
+    log(f"  layers quantized and resident in {time.perf_counter() - t0:.1f} s")
+    head, (x, w, ids, _) = run_layer(cfg, copies, T, a.steps, a.warmup, a.block)
+    log(f"  T={T}: {head['ms_per_step'] * 1e3:.1f} us/layer, {head['tokens_per_s']:.0f} tok/s, "
+        f"{head['hbm_gbps']:.0f} GB/s, kernels {head['kernels']}")
+
+    k = head["kernels"]
+    glu_gbs = head["glu_bytes"] / (k["glu_us"] * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "achieved": glu_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": glu_gbs / HBM_PEAK_GBS, "traffic": None, "kernel": "hex_moe_kernel (gate/up, SwiGLU)",
+                "algorithmic_bytes_per_launch": head["glu_bytes"], "avg_launch_us": k["glu_us"]}
+
+    sweep = {}
+    if not a.no_sweep and a.config == 2:
+        for Ts in (1, 4, 64):
+            r, _ = run_layer(cfg, copies, Ts, max(80, a.steps // 4), a.warmup, a.block, breakdown=False)
+            sweep[f"T{Ts}"] = {kk: r[kk] for kk in ("ms_per_step", "tokens_per_s", "hbm_gbps", "hbm_frac",
+                                                     "unique_experts")}
+            log(f"  T={Ts}: {r['ms_per_step'] * 1e3:.1f} us/layer, {r['hbm_gbps']:.0f} GB/s")
+        del copies
+        torch.cuda.empty_cache()
+        pf = build_tiers(CONFIGS[3], a.block, 2, dev)
+        r, _ = run_layer(CONFIGS[3], pf, 4096, 16, 4, a.block, breakdown=False)
+        sweep["config3_T4096"] = {kk: r[kk] for kk in ("ms_per_step", "tokens_per_s", "mfma_frac", "hbm_gbps",
+                                                        "unique_experts")}
+        log(f"  config3 T=4096: {r['ms_per_step']:.2f} ms/layer, MFMA {r['mfma_frac'] * 100:.1f}% of bf16 peak")
+        copies = None
+        del pf
+        torch.cuda.empty_cache()
+
+    if a.copy_calibration:
+        src = torch.empty(128 << 20, dtype=torch.bfloat16, device=dev).normal_()
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"  copy calibration: 3 x {src.numel() * 2} bytes read and written")
+        del src, dst
+
+    cpu = None
+    if not a.no_cpu_baseline:
+        base = copies[0] if copies is not None else build_tiers(cfg, a.block, 1, dev)[0]
+        cpu = cpu_baseline(cfg, base, x, w, ids)
+
+    line = {
+        "metric": "HEX MoE layer tokens/s; HBM GB/s @ decode b=16; MFMA util @ 4k prefill",
+        "value": head["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": head["steps"],
+        "warmup": a.warmup, "ms_per_step": head["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: seeded N(0,0.02) weights HEX-quantized on the GPU, bf16 N(0,1) activations, "
+                "N(0,1) router logits through the softmax top-k kernel",
+        "config": {"workload": f"{cfg['name']}, T={T} tokens, fp8 scale per {a.block} inputs, "
+                               f"{a.copies} resident layer copies cycled", "experts": cfg["E"], "hidden": cfg["H"],
+                   "moe_intermediate": cfg["I"], "top_k": cfg["k"], "bits": cfg["bits"], "block": a.block,
+                   "tokens": T, "unique_experts": head["unique_experts"], "path": "fused"},
+        "hbm_gbps_layer": head["hbm_gbps"], "hbm_frac_layer": head["hbm_frac"],
+        "kernels_us": {kk: v for kk, v in k.items() if kk.endswith("_us")}, "tiles": k["tiles"],
+        "roofline": roofline, "cpu_baseline": cpu, "sweep": sweep,
+        "gpu": torch.cuda.get_device_name(dev),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.path.insert(0, str(ROOT))
+    raise SystemExit(main())

@@ -164,18 +164,20 @@ def plan(ids: torch.Tensor, n: int, block_m: int, mode: str = "auto"):
 
 def _tile_from(cfg: dict) -> tuple[int, int]:
     """(block_m, k_split) of a config dict. BLOCK_M (slots per expert block) rounds to 16, 32 or
-    64; BLOCK_N (output rows per workgroup) 64, 32 or 16 means k_split 1, 2 or 4 (waves
-    splitting the inputs). The reference's BLOCK_K, num_warps and num_stages have no
-    counterpart here and are ignored."""
+    64; BLOCK_N (output rows per 8-wave workgroup) 128, 64 or 32 means k_split 1, 2 or 4 (waves
+    splitting the inputs), which applies to 16-slot blocks only. The reference's BLOCK_K,
+    num_warps and num_stages have no counterpart here and are ignored."""
     bm = int(cfg.get("BLOCK_M", 16))
     bm = 16 if bm <= 16 else (32 if bm <= 32 else 64)
     ks = cfg.get("K_SPLIT")
     if ks is None:
-        bn = int(cfg.get("BLOCK_N", 64))
-        ks = 4 if bn <= 16 else (2 if bn <= 32 else 1)
+        bn = int(cfg.get("BLOCK_N", 128))
+        ks = 4 if bn <= 32 else (2 if bn <= 64 else 1)
     ks = int(ks)
     if ks not in (1, 2, 4):
         raise ValueError(f"K_SPLIT must be 1, 2 or 4, got {ks}")
+    if bm > 16:
+        ks = 1          # input splitting is a decode tile (16-slot blocks)
     return bm, ks
 
 
@@ -189,16 +191,16 @@ def default_config(slots: int, n_out: int, n_in: int, glu: bool, n_experts: int 
         v = [int(t) for t in env.split(",")]
         cfg = dict(zip(("BLOCK_M", "BLOCK_N", "K_SPLIT"), v))
         bm, ks = _tile_from(cfg)
-        return {"BLOCK_M": bm, "BLOCK_N": 64 // ks, "K_SPLIT": ks}
+        return {"BLOCK_M": bm, "BLOCK_N": 128 // ks, "K_SPLIT": ks}
     per_expert = slots / max(1, n_experts or slots)
     bm = 16 if per_expert <= 16 else (32 if per_expert <= 48 else 64)
     if glu and bm == 64:
-        bm = 32      # the 4-subtile SwiGLU variant spills at 128-input scale blocks
+        bm = 32      # the 4-subtile SwiGLU variant needs 160 registers: half the waves per SIMD
     blocks = min(slots, n_experts or slots)
-    ks = 1
-    while ks < 4 and blocks * -(-n_out // (64 // ks)) < 1024:
+    ks = 2 if bm == 16 else 1
+    while bm == 16 and ks < 4 and blocks * -(-n_out // (128 // ks)) < 512:
         ks *= 2
-    return {"BLOCK_M": bm, "BLOCK_N": 64 // ks, "K_SPLIT": ks}
+    return {"BLOCK_M": bm, "BLOCK_N": 128 // ks, "K_SPLIT": ks}
 
 
 # --------------------------------------------------------------------------- fused path
@@ -209,7 +211,7 @@ def _launch_glu(x, act, t: HexTier, sid, eid, npp, S, a_div, bm, ks):
     n_out = t.gate_proj["idx"].shape[1]
     n_in = _n_in(t.gate_proj, t.bits)
     assert x.shape[1] == n_in, f"input width {x.shape[1]} != HEX width {n_in}"
-    tile = _lib.HexTile(bm, 64 // ks, ks)
+    tile = _lib.HexTile(bm, 128 // ks, ks)
     _lib.check(lib.bh_hex_moe_glu(
         x.data_ptr(), _lib.dtype_code(x.dtype), x.stride(0), act.data_ptr(), act.stride(0),
         t.struct("gate_proj"), t.struct("up_proj"), t.bits, n_out, n_in,
@@ -222,7 +224,7 @@ def _launch_down(act, y, t: HexTier, sid, eid, npp, S, w, bm, ks):
     n_out = t.down_proj["idx"].shape[1]
     n_in = _n_in(t.down_proj, t.bits)
     assert act.shape[1] == n_in, f"input width {act.shape[1]} != HEX width {n_in}"
-    tile = _lib.HexTile(bm, 64 // ks, ks)
+    tile = _lib.HexTile(bm, 128 // ks, ks)
     _lib.check(lib.bh_hex_moe_down(
         act.data_ptr(), _lib.dtype_code(act.dtype), act.stride(0), y.data_ptr(), y.stride(0),
         t.struct("down_proj"), t.bits, n_out, n_in,

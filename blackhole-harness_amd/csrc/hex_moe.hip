@@ -5,20 +5,27 @@
 // hex_moe.py:325. Designed for the decode regime, where a layer streams every routed expert's
 // packed indices once and the matrix cores have room to spare:
 //
-//  * grid = (expert blocks of the slot plan) x (output row tiles). A workgroup of 4 waves owns
-//    one expert block (16 * MT slots) and 64 / k_split output rows; the waves split the rows
-//    and, with k_split > 1, the input dimension (partials summed through LDS at the end).
+//  * Work items are (expert block of the slot plan) x (row tile of 128 / k_split output rows).
+//    The grid is persistent (two workgroups per compute unit); each workgroup takes a
+//    contiguous range of the used items, so consecutive items mostly share an expert and its
+//    LDS tables. Block experts and slot rows of the range are staged in LDS first.
+//  * A workgroup has 8 waves (4 per SIMD at two workgroups per compute unit); they split the
+//    tile's rows and, with k_split > 1, the inputs
+//    (partials summed through LDS at the end of each item).
 //  * Each lane streams the packed words of one whole 32-input block per row per step with one
 //    128-bit load (4-bit; three dwords at 3-bit): row n = lane % 16, block 4 s + lane / 16, so a
-//    step covers 128 inputs of 16 rows. A 4x4 transpose across the wave's rows (permlane swaps)
-//    then gives each lane the 8 codes the 16x16x32 MFMA wants from it, with all 32 inputs of one
-//    MFMA inside one HEX block, so every MFMA partial carries exactly one fp8 block scale.
+//    step covers 128 inputs of 16 rows. Loads run D steps ahead of the math in registers, and
+//    the pipeline runs across item boundaries, so HBM sees a steady stream of requests.
+//  * A 4x4 transpose across the wave's rows (permlane swaps) gives each lane the 8 codes the
+//    16x16x32 MFMA wants from it, with all 32 inputs of one MFMA inside one HEX block, so every
+//    MFMA partial carries exactly one fp8 block scale.
 //  * Codes resolve through a pair table in LDS: entry p = (level[p & (L-1)], level[p >> bits])
 //    rounded to the activation dtype and packed, so one ds_read_b32 yields two operands. The
 //    table has one copy per lane in its own bank (32 copies each for gate and up, 64 for down);
-//    the read address is (pair << 8) | lane copy offset, one v_perm_b32 at 4 bits.
-//  * fp32 partial of each block x its fp8 scale is added to the accumulator; the expert scale,
-//    SiLU * up, and the top-k weight are applied in the epilogue, in the reference's order.
+//    the read address is (pair << 8) | lane copy offset, one v_perm_b32 at 4 bits. It is
+//    rebuilt only when the expert changes.
+//  * The fp32 partial of each block times its fp8 scale is added to the accumulator; the expert
+//    scale, SiLU * up, and the top-k weight are applied in the epilogue, in the reference's order.
 // Weights therefore enter the matrix cores as round(level) and the block scale is applied to
 // the float32 block partial, where the reference rounds level * fp8 to the activation dtype.
 #include <string>
@@ -90,39 +97,122 @@ struct Stage {
   u32x4 ax[MT][4];       // activation fragments of the 4 MFMAs
 };
 
-template <int BITS, int ADT, bool GLU, int MT, int SB>
-__global__ __launch_bounds__(256, 2) void hex_moe_kernel(MoeArgs a) {
+// Buffer resources and per-lane byte offsets of one work item (expert block x row tile). Each
+// resource spans one expert's matrix (or the activations), so loads past its end return zero
+// instead of faulting; rows past the matrix and padding slots read data whose results are
+// never stored. The step offset goes in the scalar soffset, so a step costs no address math.
+template <int MT, int NM>
+struct ItemRes {
+  __amdgpu_buffer_rsrc_t rw[NM];   // packed index words of the item's expert
+  __amdgpu_buffer_rsrc_t rb[NM];   // its fp8 block scales
+  int vw[NM], vb[NM];              // lane offsets: row n, block 4 s + lane / 16
+  int vx[MT];                      // lane offsets into the activations: slot row, 8 inputs
+};
+
+constexpr int kRsrcWord3 = 0x00020000;   // raw buffer, 32-bit data format (gfx9 family)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
+                                           (int)(bytes > 0x7FFFFFFF ? 0x7FFFFFFF : bytes), kRsrcWord3);
+}
+
+// Expert blocks a workgroup's item range may touch (their experts and slot rows are staged in
+// LDS); the launch sizes the grid so no range needs more. At 16-slot blocks; 64 / MT in general.
+constexpr int kMaxBlk16 = 64;
+
+// Position in a workgroup's (item, step) sequence, advanced without divisions.
+struct Pos {
+  int pm;      // block, relative to the range's first block
+  int pn;      // row tile
+  int sidx;    // step of this wave within the item
+};
+
+// Prefetch depth D: steps of 128 inputs in flight per wave, also the chunk the main loop moves
+// by. With 128 registers per lane (four waves per SIMD) the gate/up kernel keeps 2 steps in
+// flight, the down kernel 3 (dividing the 6 steps of a 768-input row); 16 waves per compute
+// unit keep about as many bytes in flight as 8 waves with twice the depth, and hide twice the
+// latency of the decode-lookup-MFMA chain.
+template <int MT, bool GLU>
+constexpr int depth() { return GLU ? (MT == 1 ? 2 : 1) : (MT == 1 ? 3 : (MT == 2 ? 2 : 1)); }
+
+// floats per lane that one pass of the k-split reduction moves through LDS
+template <bool GLU>
+__host__ __device__ constexpr int red_chunk() { return GLU ? 4 : 2; }
+
+constexpr int kThreads = 512;      // 8 waves: 4 per SIMD with two workgroups per compute unit
+constexpr int kWaves = kThreads / kWave;
+
+constexpr int kOOR = 0x7FFF0000;   // byte offset past every resource: loads return zero, fetch nothing
+
+template <int BITS, int ADT, bool GLU, int MT, int SB, bool KF>
+__global__ __launch_bounds__(kThreads, (GLU && MT == 4) ? 2 : 4) void hex_moe_kernel(MoeArgs a) {
   constexpr int L = 1 << BITS;
   constexpr int NPAIR = 1 << (2 * BITS);
   constexpr int NM = GLU ? 2 : 1;
   constexpr int BM = 16 * MT;
-  constexpr int NV = MT * NM * 4;                         // accumulator floats per lane
-  constexpr int TAB = NPAIR * 64 > 192 * NV ? NPAIR * 64 : 192 * NV;
-  __shared__ __align__(16) uint32_t tab[TAB];
-  __shared__ uint32_t lvb[2][16];
+  constexpr int NV = MT * NM * 4;                          // accumulator floats per lane
+  constexpr int RCH = red_chunk<GLU>();                    // k-split partials per lane and pass
+  constexpr int D = depth<MT, GLU>();
+  constexpr int MAXBLK = kMaxBlk16 / MT;
+  // Everything a work item needs besides its streamed weights and activations is staged in LDS
+  // at the start, so the main loop issues no global load except the pipeline's, unconditionally
+  // (the hardware's in-order load counter then waits exactly as long as the data needs).
+  __shared__ __align__(16) uint32_t tab[NPAIR * 64];
+  extern __shared__ __align__(16) float red[];    // k-split partials, sized at launch (block_m 16 only)
+  __shared__ int slots[MAXBLK * BM];                               // slot rows of the range's blocks
+  __shared__ float slot_w[GLU ? 1 : MAXBLK * BM];                  // their top-k weights (down)
+  __shared__ int blk_e[MAXBLK];                                    // tier-local expert (-1: none)
+  __shared__ float blk_es[MAXBLK][NM];                             // expert scales
+  __shared__ uint16_t blk_lv[MAXBLK][NM][L];                       // levels in the activation dtype
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, ln = lane & 15, lg = lane >> 4;
-  const int pid_m = blockIdx.x, pid_n = blockIdx.y;
-  if ((int64_t)pid_m * BM >= (int64_t)a.npp[0]) return;
-  const int eg = a.eid[pid_m];
-  if (eg < 0 || eg >= a.n_experts) return;
-  const int e = a.lookup[eg];
-  if (e < 0) return;
+  const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, lg = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: steps and row tiles stay scalar
+  const int KS = a.k_split, NWN = kWaves / KS;
+  const int wn = wave % NWN, wk = wave / NWN, BN = 16 * NWN;
+  const int nrt = (a.N + BN - 1) / BN;
+  const int nb32 = a.K / kHexBlock;
+  const int nsteps = (nb32 + 3) / 4;
+  const int spw = (nsteps + KS - 1) / KS;                 // steps per wave per item (uniform)
+  const int spw_p = (spw + D - 1) / D * D;                // padded to whole chunks
+  const int s0 = wk * spw;
 
-  // ---- pair tables
-  if (tid < NM * L) {
-    const int t = tid / L, c = tid % L;
-    const float* lv = t == 0 ? a.w0.levels : a.w1.levels;
-    lvb[t][c] = to_bits<ADT>(lv[(int64_t)e * L + c]);
+  // ---- this workgroup's contiguous range of items over the used blocks
+  const int64_t used = (int64_t)a.npp[0] / BM;
+  const int64_t items = used * nrt;
+  const int64_t i0 = items * blockIdx.x / gridDim.x, i1 = items * (blockIdx.x + 1) / gridDim.x;
+  const int nitems = (int)(i1 - i0);
+  if (nitems <= 0) return;
+  const int64_t pm0 = i0 / nrt;
+  const int pn0 = (int)(i0 - pm0 * nrt);
+  const int nblk = min((int)((i1 - 1) / nrt - pm0 + 1), MAXBLK);
+
+  // ---- stage block metadata (entries past the range: no expert, padding slots)
+  for (int b = tid; b < MAXBLK; b += kThreads) {
+    int e = -1;
+    if (b < nblk) {
+      const int eg = a.eid[pm0 + b];
+      e = (eg >= 0 && eg < a.n_experts) ? a.lookup[eg] : -1;
+    }
+    blk_e[b] = e;
+#pragma unroll
+    for (int m = 0; m < NM; ++m) blk_es[b][m] = e >= 0 ? (m == 0 ? a.w0 : a.w1).expert_scale[e] : 0.f;
+  }
+  for (int r = tid; r < MAXBLK * BM; r += kThreads) {
+    const int slot = r < nblk * BM ? a.sid[pm0 * BM + r] : (int)a.num_slots;
+    slots[r] = slot;
+    if constexpr (!GLU) slot_w[r] = slot < a.num_slots ? a.topk_w[slot] : 0.f;
+  }
+  for (int i = tid; i < MAXBLK * NM * L; i += kThreads) {
+    const int b = i / (NM * L), m = (i / L) % NM, c = i % L;
+    int e = -1;
+    if (b < nblk) {
+      const int eg = a.eid[pm0 + b];
+      e = (eg >= 0 && eg < a.n_experts) ? a.lookup[eg] : -1;
+    }
+    blk_lv[b][m][c] = e >= 0 ? (uint16_t)to_bits<ADT>((m == 0 ? a.w0 : a.w1).levels[(int64_t)e * L + c]) : 0;
   }
   __syncthreads();
-  for (int base = tid * 4; base < NPAIR * 64; base += 256 * 4) {
-    const int p = base >> 6, within = base & 63;
-    const int t = GLU ? (within >> 5) : 0;
-    const uint32_t v = lvb[t][p & (L - 1)] | (lvb[t][p >> BITS] << 16);
-    *reinterpret_cast<u32x4*>(&tab[base]) = u32x4{v, v, v, v};
-  }
-  __syncthreads();
+
   uint32_t cb[NM];
   if constexpr (GLU) {
     cb[0] = (lane & 31u) * 4u;
@@ -130,79 +220,81 @@ __global__ __launch_bounds__(256, 2) void hex_moe_kernel(MoeArgs a) {
   } else {
     cb[0] = lane * 4u;
   }
+  auto advance = [&](Pos& p) {       // by one chunk
+    p.sidx += D;
+    if (p.sidx == spw_p) {
+      p.sidx = 0;
+      if (++p.pn == nrt) {
+        p.pn = 0;
+        ++p.pm;
+      }
+    }
+  };
 
-  // ---- work split
-  const int KS = a.k_split, NWN = 4 / KS;
-  const int wn = wave % NWN, wk = wave / NWN;
-  const int n = pid_n * (16 * NWN) + wn * 16 + ln;
-  const bool nvalid = n < a.N;
-  const int nb32 = a.K / kHexBlock;
-  const int nsteps = (nb32 + 3) / 4;
-  const int chunk = (nsteps + KS - 1) / KS;
-  const int s0 = wk * chunk, s1 = min(nsteps, s0 + chunk);
-
-  const uint16_t* xrow[MT];
-  bool avalid[MT];
+  // ---- load stream: buffer loads, per-item descriptors, the step in soffset
+  ItemRes<MT, NM> R;
+  const int x_rows = (int)((a.num_slots + a.a_div - 1) / a.a_div);
+  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(a.x, (int64_t)x_rows * a.s_xm * 2);
+  constexpr int WSTEP = 4 * BITS * 4;          // bytes of 4 blocks of one row
+  auto setup = [&](const Pos& p) {
+    const int b = min(p.pm, MAXBLK - 1);
+    const int e = __builtin_amdgcn_readfirstlane(blk_e[b]);   // uniform: keeps descriptors scalar
+    const int n = p.pn * BN + wn * 16 + ln;
+    const bool rv = e >= 0 && n < a.N;               // rows past the matrix fetch nothing
+    const int64_t ee = e >= 0 ? e : 0;
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int slot = a.sid[(int64_t)pid_m * BM + mt * 16 + ln];
-    avalid[mt] = slot < a.num_slots;
-    xrow[mt] = a.x + (int64_t)(avalid[mt] ? slot / a.a_div : 0) * a.s_xm;
-  }
-  const uint32_t* wp[NM];
-  const uint8_t* bsp[NM];
+    for (int m = 0; m < NM; ++m) {
+      const bh_hex_proj& w = m == 0 ? a.w0 : a.w1;
+      R.rw[m] = buffer_rsrc(w.idx + ee * w.s_ie, (int64_t)a.N * w.s_in * 4);
+      R.rb[m] = buffer_rsrc(w.block_scale + ee * w.s_be, (int64_t)a.N * w.s_bn);
+      R.vw[m] = rv ? (int)(n * w.s_in * 4) + lg * (BITS * 4) : kOOR;
+      R.vb[m] = rv ? (int)(n * w.s_bn) : kOOR;
+    }
 #pragma unroll
-  for (int m = 0; m < NM; ++m) {
-    const bh_hex_proj& w = m == 0 ? a.w0 : a.w1;
-    wp[m] = w.idx + (int64_t)e * w.s_ie + (int64_t)(nvalid ? n : 0) * w.s_in;
-    bsp[m] = w.block_scale + (int64_t)e * w.s_be + (int64_t)(nvalid ? n : 0) * w.s_bn;
-  }
-
-  auto load = [&](int s, Stage<BITS, MT, NM>& st) {
-    const int blk = 4 * s + lg;
-    const bool bv = nvalid && blk < nb32;
+    for (int mt = 0; mt < MT; ++mt) {                // padding slots fetch nothing
+      const int slot = slots[b * BM + mt * 16 + ln];
+      R.vx[mt] = (e >= 0 && slot < a.num_slots) ? (int)((int64_t)(slot / a.a_div) * a.s_xm * 2) + lg * 16 : kOOR;
+    }
+  };
+  // step j (0..spw_p-1) of the load stream's item: padded steps read out of range
+  auto load = [&](int j, Stage<BITS, MT, NM>& st) {
+    const int sr = s0 + j;
+    const bool real = j < spw && sr < nsteps;
+    const int s = __builtin_amdgcn_readfirstlane(real ? sr : 0);
+    const int ws = real ? s * WSTEP : kOOR, bs1 = real ? 4 * s : kOOR, bs4 = real ? s : kOOR;
+    const int xs = real ? s * 256 : kOOR;
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
       if constexpr (BITS == 4) {
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (bv) v = *reinterpret_cast<const u32x4*>(wp[m] + blk * 4);
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(R.rw[m], R.vw[m], ws, 0);
         st.w[m][0] = v[0]; st.w[m][1] = v[1]; st.w[m][2] = v[2]; st.w[m][3] = v[3];
       } else {
-#pragma unroll
-        for (int j = 0; j < 3; ++j) st.w[m][j] = bv ? wp[m][blk * 3 + j] : 0u;
-        st.w[m][3] = 0u;
+        const auto v = __builtin_amdgcn_raw_buffer_load_b96(R.rw[m], R.vw[m], ws, 0);
+        st.w[m][0] = v[0]; st.w[m][1] = v[1]; st.w[m][2] = v[2]; st.w[m][3] = 0u;
       }
       if constexpr (SB == 1) {
         if (a.scale_words) {
-          st.sc[m] = nvalid ? *reinterpret_cast<const uint32_t*>(bsp[m] + 4 * s) : 0u;
+          st.sc[m] = __builtin_amdgcn_raw_buffer_load_b32(R.rb[m], R.vb[m], bs1, 0);
         } else {
           uint32_t v = 0u;
 #pragma unroll
           for (int q = 0; q < 4; ++q)
-            if (nvalid && 4 * s + q < nb32) v |= (uint32_t)bsp[m][4 * s + q] << (8 * q);
+            v |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(R.rb[m], R.vb[m] + q, bs1, 0) << (8 * q);
           st.sc[m] = v;
         }
       } else {
-        st.sc[m] = nvalid ? (uint32_t)bsp[m][s] : 0u;
+        st.sc[m] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(R.rb[m], R.vb[m], bs4, 0);
       }
     }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int bq = 4 * s + q;
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (avalid[mt] && bq < nb32) v = *reinterpret_cast<const u32x4*>(xrow[mt] + bq * kHexBlock + lg * 8);
-        st.ax[mt][q] = v;
-      }
+      for (int q = 0; q < 4; ++q)
+        st.ax[mt][q] = __builtin_amdgcn_raw_buffer_load_b128(rx, R.vx[mt] + q * 64, xs, 0);
   };
 
+  // ---- compute stream
   f32x4 acc[MT][NM];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int m = 0; m < NM; ++m) acc[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
-
   auto compute = [&](int s, const Stage<BITS, MT, NM>& st) {
     uint32_t r[NM][4];
 #pragma unroll
@@ -218,7 +310,7 @@ __global__ __launch_bounds__(256, 2) void hex_moe_kernel(MoeArgs a) {
       }
       transpose_rows4(r[m]);     // r[m][q] = field lg of block 4 s + q
     }
-    const int nq = min(4, nb32 - 4 * s);
+    const int nq = KF ? 4 : min(4, nb32 - 4 * s);
     if constexpr (SB == 1) {
       float sf[NM][4];
 #pragma unroll
@@ -265,64 +357,107 @@ __global__ __launch_bounds__(256, 2) void hex_moe_kernel(MoeArgs a) {
     }
   };
 
-  // ---- main loop, one step of prefetch
-  Stage<BITS, MT, NM> st0, st1;
-  if (s0 < s1) load(s0, st0);
-  for (int s = s0; s < s1; s += 2) {
-    if (s + 1 < s1) load(s + 1, st1);
-    compute(s, st0);
-    if (s + 1 < s1) {
-      if (s + 2 < s1) load(s + 2, st0);
-      compute(s + 1, st1);
+  // pair tables of block b's expert: entry p = (level[p & (L-1)], level[p >> bits]) packed,
+  // copied into every lane's bank slot (callers hold barriers on both sides)
+  auto build_table = [&](int b) {
+#pragma unroll
+    for (int i = 0; i < NPAIR * 64 / (4 * kThreads); ++i) {
+      const int base = i * 4 * kThreads + tid * 4;
+      const int p = base >> 6, within = base & 63;
+      const int t = GLU ? (within >> 5) : 0;
+      const uint32_t v = (uint32_t)blk_lv[b][t][p & (L - 1)] | ((uint32_t)blk_lv[b][t][p >> BITS] << 16);
+      *reinterpret_cast<u32x4*>(&tab[base]) = u32x4{v, v, v, v};
     }
-  }
+  };
 
-  // ---- k-split partials through LDS
-  __syncthreads();
-  if (KS > 1) {
-    float* red = reinterpret_cast<float*>(tab);
-    if (wk > 0) {
-      float* dst = red + (int64_t)((wk - 1) * NWN + wn) * NV * 64;
+  // epilogue of one item (reference order: acc * es; silu(g) * (u * es_u); * topk weight)
+  auto epilogue = [&](const Pos& p, int e) {
+    if constexpr (MT == 1) {
+      if (KS > 1) {
+        // partials pass through LDS RCH floats per lane at a time, which keeps the area small
+        // enough for two workgroups per compute unit beside the lookup tables
+#pragma unroll
+        for (int q = 0; q < NV / RCH; ++q) {
+          __syncthreads();       // the previous pass's readers of red are done
+          if (wk > 0) {
+            float* dst = red + ((wk - 1) * NWN + wn) * RCH * 64;
+#pragma unroll
+            for (int i = 0; i < RCH; ++i) dst[i * 64 + lane] = acc[0][(q * RCH + i) / 4][(q * RCH + i) % 4];
+          }
+          __syncthreads();
+          if (wk == 0) {
+#pragma unroll
+            for (int j = 1; j < 4; ++j) {    // k_split <= 4
+              if (j < KS) {
+                const float* src = red + ((j - 1) * NWN + wn) * RCH * 64;
+#pragma unroll
+                for (int i = 0; i < RCH; ++i) acc[0][(q * RCH + i) / 4][(q * RCH + i) % 4] += src[i * 64 + lane];
+              }
+            }
+          }
+        }
+      }
+    }
+    if (wk != 0 || e < 0) return;
+    const int n = p.pn * BN + wn * 16 + ln;
+    if (n >= a.N) return;
+    const int b = min(p.pm, MAXBLK - 1);
+    const float es0 = blk_es[b][0], es1 = blk_es[b][NM - 1];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = b * BM + mt * 16 + 4 * lg + r;
+        const int slot = slots[row];
+        if (slot >= a.num_slots) continue;
+        if constexpr (GLU) {
+          const float g = acc[mt][0][r] * es0;
+          const float h = g / (1.0f + expf(-g)) * (acc[mt][1][r] * es1);
+          reinterpret_cast<uint16_t*>(a.out)[(int64_t)slot * a.s_om + n] = (uint16_t)to_bits<ADT>(h);
+        } else {
+          const float y = acc[mt][0][r] * es0 * slot_w[row];
+          reinterpret_cast<float*>(a.out)[(int64_t)slot * a.s_om + n] = y;
+        }
+      }
+  };
+
+  // ---- one pipeline over (item, chunk of D steps): loads run one chunk ahead, across item
+  // boundaries; chunks never straddle items, so control is per chunk, not per step
+  const int cpi = spw_p / D;                               // chunks per item
+  const int nchunks = nitems * cpi;
+  Stage<BITS, MT, NM> st[D];
+  Pos lp{0, pn0, 0}, cp{0, pn0, 0};
+  setup(lp);
+#pragma unroll
+  for (int d = 0; d < D; ++d) load(d, st[d]);
+  advance(lp);
+  int cur_b = -1;
+  for (int c = 0; c < nchunks; ++c) {
+    const int b = min(cp.pm, MAXBLK - 1);
+    const int e = __builtin_amdgcn_readfirstlane(blk_e[b]);
+    if (cp.sidx == 0) {
+      if (e >= 0 && (cur_b < 0 || blk_e[cur_b] != e)) {
+        __syncthreads();
+        build_table(b);
+        __syncthreads();
+        cur_b = b;
+      }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int m = 0; m < NM; ++m)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) dst[((mt * NM + m) * 4 + r) * 64 + lane] = acc[mt][m][r];
+        for (int m = 0; m < NM; ++m) acc[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    __syncthreads();
-    if (wk == 0) {
-      for (int j = 1; j < KS; ++j) {
-        const float* src = red + (int64_t)((j - 1) * NWN + wn) * NV * 64;
+    if (lp.sidx == 0) setup(lp);
+    const int sc = s0 + cp.sidx;
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int m = 0; m < NM; ++m)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[mt][m][r] += src[((mt * NM + m) * 4 + r) * 64 + lane];
-      }
+    for (int d = 0; d < D; ++d) {
+      if (e >= 0 && cp.sidx + d < spw && sc + d < nsteps) compute(sc + d, st[d]);
+      load(lp.sidx + d, st[d]);
     }
+    if (cp.sidx + D == spw_p) epilogue(cp, e);
+    advance(cp);
+    advance(lp);
   }
-  if (wk != 0 || !nvalid) return;
-
-  // ---- epilogue (reference order: acc * es; silu(g) * (u * es_u); * topk weight)
-  const float es0 = a.w0.expert_scale[e];
-  const float es1 = GLU ? a.w1.expert_scale[e] : 0.f;
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int slot = a.sid[(int64_t)pid_m * BM + mt * 16 + 4 * lg + r];
-      if (slot >= a.num_slots) continue;
-      if constexpr (GLU) {
-        const float g = acc[mt][0][r] * es0;
-        const float h = g / (1.0f + expf(-g)) * (acc[mt][1][r] * es1);
-        reinterpret_cast<uint16_t*>(a.out)[(int64_t)slot * a.s_om + n] = (uint16_t)to_bits<ADT>(h);
-      } else {
-        const float y = acc[mt][0][r] * es0 * a.topk_w[slot];
-        reinterpret_cast<float*>(a.out)[(int64_t)slot * a.s_om + n] = y;
-      }
-    }
 }
 
 // ----------------------------------------------------------------------------------- reduction
@@ -355,10 +490,23 @@ __global__ __launch_bounds__(256) void moe_reduce_kernel(const float* __restrict
 
 // ----------------------------------------------------------------------------------- host side
 
+// Dynamic LDS for the k-split partials: one reduction pass of (k_split - 1) waves per row tile.
+template <bool GLU, int MT>
+static size_t red_bytes(int ks) {
+  return ks > 1 ? (size_t)(ks - 1) * (kWaves / ks) * red_chunk<GLU>() * kWave * sizeof(float) : 16;
+}
+
 template <int BITS, int ADT, bool GLU, int MT>
 static void launch_sb(int sb, dim3 grid, hipStream_t st, const MoeArgs& a) {
-  if (sb == 1) hipLaunchKernelGGL((hex_moe_kernel<BITS, ADT, GLU, MT, 1>), grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL((hex_moe_kernel<BITS, ADT, GLU, MT, 4>), grid, dim3(256), 0, st, a);
+  const bool kf = (a.K / kHexBlock) % 4 == 0;     // whole 128-input steps: no tail checks
+  const size_t shm = red_bytes<GLU, MT>(a.k_split);
+  const dim3 block(kThreads);
+  if (sb == 1) {
+    if (kf) hipLaunchKernelGGL((hex_moe_kernel<BITS, ADT, GLU, MT, 1, true>), grid, block, shm, st, a);
+    else hipLaunchKernelGGL((hex_moe_kernel<BITS, ADT, GLU, MT, 1, false>), grid, block, shm, st, a);
+  } else {   // 128-input scale blocks imply whole steps
+    hipLaunchKernelGGL((hex_moe_kernel<BITS, ADT, GLU, MT, 4, true>), grid, block, shm, st, a);
+  }
 }
 
 template <int BITS, int ADT, bool GLU>
@@ -381,6 +529,25 @@ static void launch_moe(int bits, int adt, int mt, int sb, dim3 grid, hipStream_t
 
 static bool aligned(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
 
+// Persistent grid: at most two workgroups per compute unit (64 KB pair tables each), never more
+// than there are (expert block, row tile) items, and enough that no workgroup's contiguous item
+// range spans more expert blocks than it stages in LDS (64 / MT).
+static dim3 persistent_grid(int64_t num_blocks, int64_t n_out, int block_n, int mt) {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (!cus[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  const int64_t items = num_blocks * cdiv(n_out, block_n);
+  int64_t g = items < 2 * (int64_t)cus[dev] ? items : 2 * (int64_t)cus[dev];
+  const int64_t min_g = cdiv(num_blocks, kMaxBlk16 / mt - 2);
+  if (g < min_g) g = min_g;
+  return dim3((unsigned)(g > 0 ? g : 1));
+}
+
 // Shared argument checks of the two fused entry points; fills the plan part of MoeArgs.
 static int check_moe(const char* who, int32_t bits, int32_t adt, int64_t n_out, int64_t n_in, const int32_t* sid,
                      const int32_t* eid, int64_t num_blocks, const int32_t* npp, const int32_t* lookup,
@@ -393,14 +560,15 @@ static int check_moe(const char* who, int32_t bits, int32_t adt, int64_t n_out, 
     return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": block_m must be 16, 32 or 64");
   if (tile->k_split != 1 && tile->k_split != 2 && tile->k_split != 4)
     return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": k_split must be 1, 2 or 4");
-  if (tile->block_n != 64 / tile->k_split)
-    return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": block_n must be 64 / k_split");
+  if (tile->block_n != 128 / tile->k_split)
+    return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": block_n must be 128 / k_split");
+  if (tile->k_split > 1 && tile->block_m != 16)
+    return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": k_split > 1 needs block_m 16");
   if (n_out <= 0 || n_out > (1 << 30) || n_in > (1 << 30)) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": bad width");
   if (n_experts <= 0 || num_slots < 0 || num_blocks < 0 || num_blocks > INT32_MAX)
     return fail(BH_HEX_ERR_VALUE, std::string(who) + ": bad plan sizes");
   if (num_blocks > 0 && (!sid || !eid || !npp || !lookup))
     return fail(BH_HEX_ERR_VALUE, std::string(who) + ": null plan pointer");
-  if (cdiv(n_out, tile->block_n) > 65535) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": too many row tiles");
   *mt = tile->block_m / 16;
   a.sid = sid;
   a.eid = eid;
@@ -458,7 +626,7 @@ extern "C" int bh_hex_moe_glu(const void* x, int32_t x_dtype, int64_t s_xm, void
   a.w1 = *up;
   a.a_div = a_div;
   a.scale_words = words;
-  const dim3 grid((unsigned)num_blocks, (unsigned)cdiv(n_out, tile->block_n));
+  const dim3 grid = persistent_grid(num_blocks, n_out, tile->block_n, mt);
   launch_moe<true>(bits, x_dtype, mt, sb, grid, reinterpret_cast<hipStream_t>(stream), a);
   return check_launch(who);
 }
@@ -487,7 +655,7 @@ extern "C" int bh_hex_moe_down(const void* act, int32_t act_dtype, int64_t s_am,
   a.topk_w = topk_w;
   a.a_div = 1;
   a.scale_words = words;
-  const dim3 grid((unsigned)num_blocks, (unsigned)cdiv(n_out, tile->block_n));
+  const dim3 grid = persistent_grid(num_blocks, n_out, tile->block_n, mt);
   launch_moe<false>(bits, act_dtype, mt, sb, grid, reinterpret_cast<hipStream_t>(stream), a);
   return check_launch(who);
 }

@@ -63,9 +63,9 @@ typedef struct bh_hex_proj {
 } bh_hex_proj;
 
 /* Tile choice of the fused kernels (the config dict of hex_moe.py:264-283, CDNA4 terms):
- * block_m slots per expert block (a multiple of 16), block_n output rows per workgroup
- * (a multiple of 16), k_split waves sharing one output tile along the input dimension
- * (1, 2 or 4). */
+ * block_m slots per expert block (16, 32 or 64), k_split waves sharing one 16-row output
+ * tile along the input dimension (1, 2 or 4; above 1 only with block_m 16), block_n output
+ * rows per 8-wave workgroup, which must be 128 / k_split. */
 typedef struct bh_hex_tile {
   int32_t block_m;
   int32_t block_n;

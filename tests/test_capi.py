@@ -71,7 +71,11 @@ def test_host_side_errors():
     _status(lib.bh_hex_moe_glu(16, _lib.BF16, 64, 16, 64, ctypes.byref(w), ctypes.byref(w), 4, 64, 64,
                                16, 16, 1, 16, 16, 4, 4, 1, ctypes.byref(tile), None),
             _lib.ERR_UNSUPPORTED, "block_n")
-    tile = _lib.HexTile(16, 64, 1)
+    tile = _lib.HexTile(32, 64, 2)
+    _status(lib.bh_hex_moe_glu(16, _lib.BF16, 64, 16, 64, ctypes.byref(w), ctypes.byref(w), 4, 64, 64,
+                               16, 16, 1, 16, 16, 4, 4, 1, ctypes.byref(tile), None),
+            _lib.ERR_UNSUPPORTED, "block_m 16")
+    tile = _lib.HexTile(16, 128, 1)
     _status(lib.bh_hex_moe_glu(16, _lib.F32, 64, 16, 64, ctypes.byref(w), ctypes.byref(w), 4, 64, 64,
                                16, 16, 1, 16, 16, 4, 4, 1, ctypes.byref(tile), None),
             _lib.ERR_UNSUPPORTED, "BF16 or F16")
