@@ -164,8 +164,8 @@ def kernel_breakdown(cfg, copies, x, w, ids, reps):
     flat = ids.reshape(-1)
     c1 = hm.default_config(S, I, H, True, E)
     c2 = hm.default_config(S, H, I, False, E)
-    bm1, ks1 = hm._tile_from(c1)
-    bm2, ks2 = hm._tile_from(c2)
+    bm1 = hm._tile_from(c1)
+    bm2 = hm._tile_from(c2)
     p1 = hm.plan(flat, E, bm1)
     p2 = hm.plan(flat, E, bm2)
     act = torch.empty(S, I, dtype=x.dtype, device=x.device)
@@ -177,12 +177,12 @@ def kernel_breakdown(cfg, copies, x, w, ids, reps):
     def glu():
         for tiers in copies:
             for t in tiers:
-                hm._launch_glu(x, act, t, *p1, S, k, bm1, ks1)
+                hm._launch_glu(x, act, t, *p1, S, k, bm1)
 
     def down():
         for tiers in copies:
             for t in tiers:
-                hm._launch_down(act, y, t, *p2, S, wf, bm2, ks2)
+                hm._launch_down(act, y, t, *p2, S, wf, bm2)
 
     def plan():
         for _ in copies:

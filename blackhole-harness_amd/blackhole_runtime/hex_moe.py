@@ -162,74 +162,77 @@ def plan(ids: torch.Tensor, n: int, block_m: int, mode: str = "auto"):
 # --------------------------------------------------------------------------- tiles
 
 
-def _tile_from(cfg: dict) -> tuple[int, int]:
-    """(block_m, k_split) of a config dict. BLOCK_M (slots per expert block) rounds to 16, 32 or
-    64; BLOCK_N (output rows per 8-wave workgroup) 128, 64 or 32 means k_split 1, 2 or 4 (waves
-    splitting the inputs), which applies to 16-slot blocks only. The reference's BLOCK_K,
-    num_warps and num_stages have no counterpart here and are ignored."""
+def _tile_from(cfg: dict) -> int:
+    """block_m of a config dict: BLOCK_M (slots per expert block) rounded to 16, 32 or 64. The
+    reference's BLOCK_N, BLOCK_K, num_warps and num_stages have no counterpart here (a work item
+    is always 256 output rows, and the kernels split the inputs between workgroups themselves)
+    and are ignored."""
     bm = int(cfg.get("BLOCK_M", 16))
-    bm = 16 if bm <= 16 else (32 if bm <= 32 else 64)
-    ks = cfg.get("K_SPLIT")
-    if ks is None:
-        bn = int(cfg.get("BLOCK_N", 128))
-        ks = 4 if bn <= 32 else (2 if bn <= 64 else 1)
-    ks = int(ks)
-    if ks not in (1, 2, 4):
-        raise ValueError(f"K_SPLIT must be 1, 2 or 4, got {ks}")
-    if bm > 16:
-        ks = 1          # input splitting is a decode tile (16-slot blocks)
-    return bm, ks
+    return 16 if bm <= 16 else (32 if bm <= 32 else 64)
 
 
 def default_config(slots: int, n_out: int, n_in: int, glu: bool, n_experts: int = 0) -> dict:
-    """Tile choice by slot count (hex_moe.py:264-283), or BLACKHOLE_HEX_TILES="BM,BN[,KS]".
-    BLOCK_M grows with the slots each expert gets, so an expert's weights are streamed by few
-    blocks; K_SPLIT splits the inputs over the workgroup's waves when too few (expert block,
-    row tile) pairs would otherwise fill the 256 compute units."""
+    """Tile choice by slot count (hex_moe.py:264-283), or BLACKHOLE_HEX_TILES="BM". BLOCK_M grows
+    with the slots each expert gets, so an expert's weights are streamed by few blocks."""
     env = os.environ.get("BLACKHOLE_HEX_TILES")
     if env:
-        v = [int(t) for t in env.split(",")]
-        cfg = dict(zip(("BLOCK_M", "BLOCK_N", "K_SPLIT"), v))
-        bm, ks = _tile_from(cfg)
-        return {"BLOCK_M": bm, "BLOCK_N": 128 // ks, "K_SPLIT": ks}
-    per_expert = slots / max(1, n_experts or slots)
-    bm = 16 if per_expert <= 16 else (32 if per_expert <= 48 else 64)
-    if glu and bm == 64:
-        bm = 32      # the 4-subtile SwiGLU variant needs 160 registers: half the waves per SIMD
-    blocks = min(slots, n_experts or slots)
-    ks = 2 if bm == 16 else 1
-    while bm == 16 and ks < 4 and blocks * -(-n_out // (128 // ks)) < 512:
-        ks *= 2
-    return {"BLOCK_M": bm, "BLOCK_N": 128 // ks, "K_SPLIT": ks}
+        bm = _tile_from({"BLOCK_M": int(env.split(",")[0])})
+    else:
+        per_expert = slots / max(1, n_experts or slots)
+        bm = 16 if per_expert <= 16 else (32 if per_expert <= 48 else 64)
+    return {"BLOCK_M": bm, "BLOCK_N": 256}
 
 
 # --------------------------------------------------------------------------- fused path
 
+_WORKSPACES: dict = {}
 
-def _launch_glu(x, act, t: HexTier, sid, eid, npp, S, a_div, bm, ks):
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Zero-filled device workspace of at least nbytes for the fused kernels on the current
+    stream. The kernels leave it zero-filled, so it is kept per (device, stream) and grown when
+    needed; one stream's calls run in order, so they never share it concurrently. Inside graph
+    capture a missing or small workspace is allocated in the graph's pool (zeroed by a captured
+    fill on every replay) and not kept."""
+    stream = torch.cuda.current_stream(device)
+    key = (device.index, stream.cuda_stream)
+    ws = _WORKSPACES.get(key)
+    if ws is not None and ws.numel() >= nbytes:
+        return ws
+    ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+    if not torch.cuda.is_current_stream_capturing():
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def _launch_glu(x, act, t: HexTier, sid, eid, npp, S, a_div, bm):
     lib = _lib.load()
     n_out = t.gate_proj["idx"].shape[1]
     n_in = _n_in(t.gate_proj, t.bits)
     assert x.shape[1] == n_in, f"input width {x.shape[1]} != HEX width {n_in}"
-    tile = _lib.HexTile(bm, 128 // ks, ks)
+    tile = _lib.HexTile(bm, 256, 1)
+    nbytes = lib.bh_hex_moe_workspace_bytes(eid.numel(), n_out, n_in, bm, 1)
+    ws = _workspace(x.device, nbytes)
     _lib.check(lib.bh_hex_moe_glu(
         x.data_ptr(), _lib.dtype_code(x.dtype), x.stride(0), act.data_ptr(), act.stride(0),
         t.struct("gate_proj"), t.struct("up_proj"), t.bits, n_out, n_in,
         sid.data_ptr(), eid.data_ptr(), eid.numel(), npp.data_ptr(), t.lookup.data_ptr(), t.lookup.numel(), S, a_div,
-        tile, _lib.stream_of(x)), "bh_hex_moe_glu")
+        tile, ws.data_ptr(), ws.numel(), _lib.stream_of(x)), "bh_hex_moe_glu")
 
 
-def _launch_down(act, y, t: HexTier, sid, eid, npp, S, w, bm, ks):
+def _launch_down(act, y, t: HexTier, sid, eid, npp, S, w, bm):
     lib = _lib.load()
     n_out = t.down_proj["idx"].shape[1]
     n_in = _n_in(t.down_proj, t.bits)
     assert act.shape[1] == n_in, f"input width {act.shape[1]} != HEX width {n_in}"
-    tile = _lib.HexTile(bm, 128 // ks, ks)
+    tile = _lib.HexTile(bm, 256, 1)
+    nbytes = lib.bh_hex_moe_workspace_bytes(eid.numel(), n_out, n_in, bm, 0)
+    ws = _workspace(act.device, nbytes)
     _lib.check(lib.bh_hex_moe_down(
         act.data_ptr(), _lib.dtype_code(act.dtype), act.stride(0), y.data_ptr(), y.stride(0),
         t.struct("down_proj"), t.bits, n_out, n_in,
         sid.data_ptr(), eid.data_ptr(), eid.numel(), npp.data_ptr(), t.lookup.data_ptr(), t.lookup.numel(), S,
-        w.data_ptr(), tile, _lib.stream_of(act)), "bh_hex_moe_down")
+        w.data_ptr(), tile, ws.data_ptr(), ws.numel(), _lib.stream_of(act)), "bh_hex_moe_down")
 
 
 def _covers_all(tiers: list[HexTier]) -> bool:
@@ -267,14 +270,14 @@ def hex_moe_fused(x, topk_weights, topk_ids, tiers: list[HexTier], config: dict 
     y = (torch.empty if _covers_all(tiers) else torch.zeros)(S, H, dtype=torch.float32, device=x.device)
     c1 = config or default_config(S, I, H, True, E)
     c2 = config or default_config(S, H, I, False, E)
-    bm1, ks1 = _tile_from(c1)
-    bm2, ks2 = _tile_from(c2)
+    bm1 = _tile_from(c1)
+    bm2 = _tile_from(c2)
     p1 = plan(flat, E, bm1, align_mode)
     p2 = p1 if bm2 == bm1 else plan(flat, E, bm2, align_mode)
     for t in tiers:
-        _launch_glu(x, act, t, *p1, S, k, bm1, ks1)
+        _launch_glu(x, act, t, *p1, S, k, bm1)
     for t in tiers:
-        _launch_down(act, y, t, *p2, S, w, bm2, ks2)
+        _launch_down(act, y, t, *p2, S, w, bm2)
     ids, code = _ids_arg(flat)
     lib = _lib.load()
     _lib.check(lib.bh_hex_moe_reduce(y.data_ptr(), y.stride(0), ids.data_ptr(), code, E, T, k, H, out.data_ptr(),

@@ -5,17 +5,19 @@
 // hex_moe.py:325. Designed for the decode regime, where a layer streams every routed expert's
 // packed indices once and the matrix cores have room to spare:
 //
-//  * Work items are (expert block of the slot plan) x (row tile of 128 / k_split output rows).
-//    The grid is persistent (two workgroups per compute unit); each workgroup takes a
-//    contiguous range of the used items, so consecutive items mostly share an expert and its
-//    LDS tables. Block experts and slot rows of the range are staged in LDS first.
-//  * A workgroup has 8 waves (4 per SIMD at two workgroups per compute unit); they split the
-//    tile's rows and, with k_split > 1, the inputs
-//    (partials summed through LDS at the end of each item).
-//  * Each lane streams the packed words of one whole 32-input block per row per step with one
-//    128-bit load (4-bit; three dwords at 3-bit): row n = lane % 16, block 4 s + lane / 16, so a
-//    step covers 128 inputs of 16 rows. Loads run D steps ahead of the math in registers, and
-//    the pipeline runs across item boundaries, so HBM sees a steady stream of requests.
+//  * Units of work are (expert block of the slot plan, 256-row tile, 128-input step). The grid
+//    is persistent, one 16-wave workgroup per compute unit, and workgroup g takes the contiguous
+//    unit range [U g / G, U (g + 1) / G): every workgroup streams the same number of steps, and
+//    consecutive units mostly share an expert and its LDS tables. An item (block, row tile)
+//    split between workgroups is finished by the last of them to arrive, which adds the others'
+//    partial sums (left in a workspace with device-coherent stores) in workgroup order, so the
+//    result does not depend on timing.
+//  * Each wave owns 16 rows of the tile. Each lane streams the packed words of one whole
+//    32-input block per row per step with one 128-bit load (4-bit; three dwords at 3-bit):
+//    row = lane % 16, block 4 s + lane / 16. Loads run P steps ahead of the math in registers,
+//    across item boundaries, so HBM sees a steady stream of requests.
+//  * The step's activation tile (16 slots x 128 inputs per 16-slot subtile) is fetched once per
+//    workgroup, a dword per lane, and passed through a two-stage LDS ring to all 16 waves.
 //  * A 4x4 transpose across the wave's rows (permlane swaps) gives each lane the 8 codes the
 //    16x16x32 MFMA wants from it, with all 32 inputs of one MFMA inside one HEX block, so every
 //    MFMA partial carries exactly one fp8 block scale.
@@ -51,8 +53,9 @@ struct MoeArgs {
   int32_t n_experts;
   int32_t a_div;
   int32_t N, K;
-  int32_t k_split;
   int32_t scale_words;   // block_scale rows allow 32-bit loads of 4 scales
+  float* part;           // workspace: partial sums of items split between workgroups
+  int* counters;         // workspace: arrivals per (item, wave), zero between calls
 };
 
 // Four fp8 scales (one byte each) -> float, by the conversion instruction; a wave holding a
@@ -94,7 +97,7 @@ template <int BITS, int MT, int NM>
 struct Stage {
   uint32_t w[NM][4];     // 4-bit: the block's 4 words; 3-bit: its 3 words
   uint32_t sc[NM];       // block scales: 4 bytes (one per MFMA) or 1 byte (128-input block)
-  u32x4 ax[MT][4];       // activation fragments of the 4 MFMAs
+  uint32_t ax[MT];       // this lane's dword of the step's activation tile (shared through LDS)
 };
 
 // Buffer resources and per-lane byte offsets of one work item (expert block x row tile). Each
@@ -106,112 +109,98 @@ struct ItemRes {
   __amdgpu_buffer_rsrc_t rw[NM];   // packed index words of the item's expert
   __amdgpu_buffer_rsrc_t rb[NM];   // its fp8 block scales
   int vw[NM], vb[NM];              // lane offsets: row n, block 4 s + lane / 16
-  int vx[MT];                      // lane offsets into the activations: slot row, 8 inputs
+  int vx[MT];                      // lane offsets into the activations: its dword of the tile
 };
 
 constexpr int kRsrcWord3 = 0x00020000;   // raw buffer, 32-bit data format (gfx9 family)
+constexpr int kCohere = 16;              // cache policy sc1: coherent across the device's L2s
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int64_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
                                            (int)(bytes > 0x7FFFFFFF ? 0x7FFFFFFF : bytes), kRsrcWord3);
 }
 
-// Expert blocks a workgroup's item range may touch (their experts and slot rows are staged in
+// Expert blocks a workgroup's unit range may touch (their experts and slot rows are staged in
 // LDS); the launch sizes the grid so no range needs more. At 16-slot blocks; 64 / MT in general.
 constexpr int kMaxBlk16 = 64;
+constexpr int kMaxExperts = 1024;        // global expert ids the tier lookup may take
 
-// Position in a workgroup's (item, step) sequence, advanced without divisions.
-struct Pos {
-  int pm;      // block, relative to the range's first block
-  int pn;      // row tile
-  int sidx;    // step of this wave within the item
-};
-
-// Prefetch depth D: steps of 128 inputs in flight per wave, also the chunk the main loop moves
-// by. With 128 registers per lane (four waves per SIMD) the gate/up kernel keeps 2 steps in
-// flight, the down kernel 3 (dividing the 6 steps of a 768-input row); 16 waves per compute
-// unit keep about as many bytes in flight as 8 waves with twice the depth, and hide twice the
-// latency of the decode-lookup-MFMA chain.
-template <int MT, bool GLU>
-constexpr int depth() { return GLU ? (MT == 1 ? 2 : 1) : (MT == 1 ? 3 : (MT == 2 ? 2 : 1)); }
-
-// floats per lane that one pass of the k-split reduction moves through LDS
-template <bool GLU>
-__host__ __device__ constexpr int red_chunk() { return GLU ? 4 : 2; }
-
-constexpr int kThreads = 512;      // 8 waves: 4 per SIMD with two workgroups per compute unit
+constexpr int kThreads = 1024;           // 16 waves, one workgroup per compute unit
 constexpr int kWaves = kThreads / kWave;
+constexpr int kRows = 16 * kWaves;       // output rows of one work item: 16 per wave
+constexpr int kMinUnits = 4;             // steps per workgroup below which the grid shrinks
+
+// Prefetch depth P: steps whose weights are in flight per wave (registers) ahead of the math.
+template <int MT, bool GLU>
+constexpr int depth() { return GLU ? (MT == 1 ? 3 : (MT == 2 ? 2 : 1)) : (MT == 1 ? 4 : (MT == 2 ? 3 : 2)); }
 
 constexpr int kOOR = 0x7FFF0000;   // byte offset past every resource: loads return zero, fetch nothing
 
+// Position of a unit: block (relative to the range's first), row tile, step.
+struct Pos {
+  int pm, pn, s;
+};
+
+// Partial sums of one wave's 16 x BM tile, [mt][m][lane][4] floats.
+template <int MT, int NM>
+constexpr int part_floats() { return MT * NM * kWave * 4; }
+
+// Work decomposition shared by the host (grid, workspace) and the kernel: units are
+// (expert block, 256-row tile, 128-input step) in that order; workgroup g takes units
+// [U g / G, U (g + 1) / G). An item (block, row tile) split between workgroups is summed by the
+// last of them to finish, in workgroup order, from partials in the workspace.
+__device__ __forceinline__ int owner(int64_t u, int64_t U, int64_t G) {
+  return (int)(((u + 1) * G + U - 1) / U - 1);
+}
+
 template <int BITS, int ADT, bool GLU, int MT, int SB, bool KF>
-__global__ __launch_bounds__(kThreads, (GLU && MT == 4) ? 2 : 4) void hex_moe_kernel(MoeArgs a) {
+__global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
   constexpr int L = 1 << BITS;
   constexpr int NPAIR = 1 << (2 * BITS);
   constexpr int NM = GLU ? 2 : 1;
   constexpr int BM = 16 * MT;
-  constexpr int NV = MT * NM * 4;                          // accumulator floats per lane
-  constexpr int RCH = red_chunk<GLU>();                    // k-split partials per lane and pass
-  constexpr int D = depth<MT, GLU>();
+  constexpr int P = depth<MT, GLU>();
   constexpr int MAXBLK = kMaxBlk16 / MT;
-  // Everything a work item needs besides its streamed weights and activations is staged in LDS
-  // at the start, so the main loop issues no global load except the pipeline's, unconditionally
-  // (the hardware's in-order load counter then waits exactly as long as the data needs).
+  constexpr int PF = part_floats<MT, NM>();
+  // Everything a unit needs besides its streamed weights and activations is staged in LDS at
+  // the start; the activation tile of each step goes through a two-stage LDS ring, loaded once
+  // per workgroup (a dword per lane) and read by all 16 waves.
   __shared__ __align__(16) uint32_t tab[NPAIR * 64];
-  extern __shared__ __align__(16) float red[];    // k-split partials, sized at launch (block_m 16 only)
+  __shared__ __align__(16) uint32_t ring[2][MT * 1024];
+  __shared__ int lut[kMaxExperts];                                 // the tier lookup
   __shared__ int slots[MAXBLK * BM];                               // slot rows of the range's blocks
   __shared__ float slot_w[GLU ? 1 : MAXBLK * BM];                  // their top-k weights (down)
-  __shared__ int blk_e[MAXBLK];                                    // tier-local expert (-1: none)
+  __shared__ int blk_g[MAXBLK];                                    // global expert of each block
   __shared__ float blk_es[MAXBLK][NM];                             // expert scales
   __shared__ uint16_t blk_lv[MAXBLK][NM][L];                       // levels in the activation dtype
 
   const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, lg = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: steps and row tiles stay scalar
-  const int KS = a.k_split, NWN = kWaves / KS;
-  const int wn = wave % NWN, wk = wave / NWN, BN = 16 * NWN;
-  const int nrt = (a.N + BN - 1) / BN;
+  const int nrt = (a.N + kRows - 1) / kRows;
   const int nb32 = a.K / kHexBlock;
   const int nsteps = (nb32 + 3) / 4;
-  const int spw = (nsteps + KS - 1) / KS;                 // steps per wave per item (uniform)
-  const int spw_p = (spw + D - 1) / D * D;                // padded to whole chunks
-  const int s0 = wk * spw;
 
-  // ---- this workgroup's contiguous range of items over the used blocks
+  // ---- this workgroup's contiguous range of units over the used blocks
   const int64_t used = (int64_t)a.npp[0] / BM;
-  const int64_t items = used * nrt;
-  const int64_t i0 = items * blockIdx.x / gridDim.x, i1 = items * (blockIdx.x + 1) / gridDim.x;
-  const int nitems = (int)(i1 - i0);
-  if (nitems <= 0) return;
-  const int64_t pm0 = i0 / nrt;
-  const int pn0 = (int)(i0 - pm0 * nrt);
-  const int nblk = min((int)((i1 - 1) / nrt - pm0 + 1), MAXBLK);
+  const int64_t U = used * nrt * nsteps;
+  const int64_t G = min((int64_t)gridDim.x, U), g = blockIdx.x;   // no workgroup has an empty range
+  if (g >= G) return;
+  const int64_t ub = U * g / G, ue = U * (g + 1) / G;
+  const int n = (int)(ue - ub);
+  const int64_t item0 = ub / nsteps;
+  const int64_t pm0 = item0 / nrt;
+  const int nblk = min((int)((ue - 1) / nsteps / nrt - pm0 + 1), MAXBLK);
 
-  // ---- stage block metadata (entries past the range: no expert, padding slots)
-  for (int b = tid; b < MAXBLK; b += kThreads) {
-    int e = -1;
-    if (b < nblk) {
-      const int eg = a.eid[pm0 + b];
-      e = (eg >= 0 && eg < a.n_experts) ? a.lookup[eg] : -1;
-    }
-    blk_e[b] = e;
-#pragma unroll
-    for (int m = 0; m < NM; ++m) blk_es[b][m] = e >= 0 ? (m == 0 ? a.w0 : a.w1).expert_scale[e] : 0.f;
-  }
-  for (int r = tid; r < MAXBLK * BM; r += kThreads) {
-    const int slot = r < nblk * BM ? a.sid[pm0 * BM + r] : (int)a.num_slots;
-    slots[r] = slot;
-    if constexpr (!GLU) slot_w[r] = slot < a.num_slots ? a.topk_w[slot] : 0.f;
-  }
-  for (int i = tid; i < MAXBLK * NM * L; i += kThreads) {
-    const int b = i / (NM * L), m = (i / L) % NM, c = i % L;
-    int e = -1;
-    if (b < nblk) {
-      const int eg = a.eid[pm0 + b];
-      e = (eg >= 0 && eg < a.n_experts) ? a.lookup[eg] : -1;
-    }
-    blk_lv[b][m][c] = e >= 0 ? (uint16_t)to_bits<ADT>((m == 0 ? a.w0 : a.w1).levels[(int64_t)e * L + c]) : 0;
-  }
+  // ---- stage the plan: tier lookup, block experts, slot rows
+  for (int i = tid; i < a.n_experts; i += kThreads) lut[i] = a.lookup[i];
+  for (int b = tid; b < MAXBLK; b += kThreads) blk_g[b] = b < nblk ? a.eid[pm0 + b] : -1;
+  for (int r = tid; r < MAXBLK * BM; r += kThreads)
+    slots[r] = r < nblk * BM ? a.sid[pm0 * BM + r] : (int)a.num_slots;
   __syncthreads();
+  auto expert_of = [&](int b) {      // tier-local expert of block b, -1 for none
+    const int eg = blk_g[b];
+    return (eg >= 0 && eg < a.n_experts) ? lut[eg] : -1;
+  };
 
   uint32_t cb[NM];
   if constexpr (GLU) {
@@ -220,10 +209,9 @@ __global__ __launch_bounds__(kThreads, (GLU && MT == 4) ? 2 : 4) void hex_moe_ke
   } else {
     cb[0] = lane * 4u;
   }
-  auto advance = [&](Pos& p) {       // by one chunk
-    p.sidx += D;
-    if (p.sidx == spw_p) {
-      p.sidx = 0;
+  auto advance = [&](Pos& p) {
+    if (++p.s == nsteps) {
+      p.s = 0;
       if (++p.pn == nrt) {
         p.pn = 0;
         ++p.pm;
@@ -235,34 +223,37 @@ __global__ __launch_bounds__(kThreads, (GLU && MT == 4) ? 2 : 4) void hex_moe_ke
   ItemRes<MT, NM> R;
   const int x_rows = (int)((a.num_slots + a.a_div - 1) / a.a_div);
   const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(a.x, (int64_t)x_rows * a.s_xm * 2);
+  // this lane's dword of a step's activation tile: wave w, lane l -> slot l / 4 of the tile,
+  // inputs 32 (w / 4) + 8 (w % 4) + 2 (l % 4) of the step (the fragment layout the MFMA reads)
+  const int xcol = (wave >> 2) * 64 + (wave & 3) * 16 + (lane & 3) * 4;
   constexpr int WSTEP = 4 * BITS * 4;          // bytes of 4 blocks of one row
   auto setup = [&](const Pos& p) {
     const int b = min(p.pm, MAXBLK - 1);
-    const int e = __builtin_amdgcn_readfirstlane(blk_e[b]);   // uniform: keeps descriptors scalar
-    const int n = p.pn * BN + wn * 16 + ln;
-    const bool rv = e >= 0 && n < a.N;               // rows past the matrix fetch nothing
+    const int e = __builtin_amdgcn_readfirstlane(expert_of(b));   // uniform: keeps descriptors scalar
+    const int nrow = p.pn * kRows + wave * 16 + ln;
+    const bool rv = e >= 0 && nrow < a.N;            // rows past the matrix fetch nothing
     const int64_t ee = e >= 0 ? e : 0;
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
       const bh_hex_proj& w = m == 0 ? a.w0 : a.w1;
       R.rw[m] = buffer_rsrc(w.idx + ee * w.s_ie, (int64_t)a.N * w.s_in * 4);
       R.rb[m] = buffer_rsrc(w.block_scale + ee * w.s_be, (int64_t)a.N * w.s_bn);
-      R.vw[m] = rv ? (int)(n * w.s_in * 4) + lg * (BITS * 4) : kOOR;
-      R.vb[m] = rv ? (int)(n * w.s_bn) : kOOR;
+      R.vw[m] = rv ? (int)(nrow * w.s_in * 4) + lg * (BITS * 4) : kOOR;
+      R.vb[m] = rv ? (int)(nrow * w.s_bn) : kOOR;
     }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {                // padding slots fetch nothing
-      const int slot = slots[b * BM + mt * 16 + ln];
-      R.vx[mt] = (e >= 0 && slot < a.num_slots) ? (int)((int64_t)(slot / a.a_div) * a.s_xm * 2) + lg * 16 : kOOR;
+      const int slot = slots[b * BM + mt * 16 + (lane >> 2)];
+      R.vx[mt] = (e >= 0 && slot < a.num_slots) ? (int)((int64_t)(slot / a.a_div) * a.s_xm * 2) + xcol : kOOR;
     }
   };
-  // step j (0..spw_p-1) of the load stream's item: padded steps read out of range
-  auto load = [&](int j, Stage<BITS, MT, NM>& st) {
-    const int sr = s0 + j;
-    const bool real = j < spw && sr < nsteps;
-    const int s = __builtin_amdgcn_readfirstlane(real ? sr : 0);
+  // loads of step s of the current descriptors; dummy steps (past the range) read out of range
+  auto load = [&](int s_, bool real, Stage<BITS, MT, NM>& st) {
+    const int s = __builtin_amdgcn_readfirstlane(real ? s_ : 0);
     const int ws = real ? s * WSTEP : kOOR, bs1 = real ? 4 * s : kOOR, bs4 = real ? s : kOOR;
     const int xs = real ? s * 256 : kOOR;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) st.ax[mt] = __builtin_amdgcn_raw_buffer_load_b32(rx, R.vx[mt], xs, 0);
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
       if constexpr (BITS == 4) {
@@ -286,16 +277,11 @@ __global__ __launch_bounds__(kThreads, (GLU && MT == 4) ? 2 : 4) void hex_moe_ke
         st.sc[m] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(R.rb[m], R.vb[m], bs4, 0);
       }
     }
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        st.ax[mt][q] = __builtin_amdgcn_raw_buffer_load_b128(rx, R.vx[mt] + q * 64, xs, 0);
   };
 
   // ---- compute stream
   f32x4 acc[MT][NM];
-  auto compute = [&](int s, const Stage<BITS, MT, NM>& st) {
+  auto compute = [&](int s, const Stage<BITS, MT, NM>& st, const uint32_t* tile) {
     uint32_t r[NM][4];
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
@@ -311,48 +297,43 @@ __global__ __launch_bounds__(kThreads, (GLU && MT == 4) ? 2 : 4) void hex_moe_ke
       transpose_rows4(r[m]);     // r[m][q] = field lg of block 4 s + q
     }
     const int nq = KF ? 4 : min(4, nb32 - 4 * s);
+    float sf[NM][4];
     if constexpr (SB == 1) {
-      float sf[NM][4];
 #pragma unroll
       for (int m = 0; m < NM; ++m) fp8x4(st.sc[m], sf[m]);
+    }
+    f32x4 part[MT][NM];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (q < nq) {
-          u32x4 b[NM];
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-          for (int m = 0; m < NM; ++m) b[m] = lookup8<BITS>(r[m][q], cb[m], tab);
+      for (int m = 0; m < NM; ++m) part[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
+    for (int q = 0; q < 4; ++q) {
+      if (q < nq) {
+        u32x4 b[NM];
 #pragma unroll
-            for (int m = 0; m < NM; ++m) {
-              const f32x4 p = mfma16x16x32<ADT>(st.ax[mt][q], b[m], f32x4{0.f, 0.f, 0.f, 0.f});
+        for (int m = 0; m < NM; ++m) b[m] = lookup8<BITS>(r[m][q], cb[m], tab);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const u32x4 ax = *reinterpret_cast<const u32x4*>(tile + mt * 1024 + q * 256 + lane * 4);
+#pragma unroll
+          for (int m = 0; m < NM; ++m) {
+            if constexpr (SB == 1) {
+              const f32x4 p = mfma16x16x32<ADT>(ax, b[m], f32x4{0.f, 0.f, 0.f, 0.f});
               acc[mt][m] += p * sf[m][q];
+            } else {
+              part[mt][m] = mfma16x16x32<ADT>(ax, b[m], part[mt][m]);
             }
+          }
         }
       }
-    } else {
-      f32x4 part[MT][NM];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int m = 0; m < NM; ++m) part[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (q < nq) {
-          u32x4 b[NM];
-#pragma unroll
-          for (int m = 0; m < NM; ++m) b[m] = lookup8<BITS>(r[m][q], cb[m], tab);
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int m = 0; m < NM; ++m) part[mt][m] = mfma16x16x32<ADT>(st.ax[mt][q], b[m], part[mt][m]);
-        }
-      }
+    }
+    if constexpr (SB == 4) {
 #pragma unroll
       for (int m = 0; m < NM; ++m) {
-        const float sf = fp8x1(st.sc[m]);
+        const float f = fp8x1(st.sc[m]);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[mt][m] += part[mt][m] * sf;
+        for (int mt = 0; mt < MT; ++mt) acc[mt][m] += part[mt][m] * f;
       }
     }
   };
@@ -370,38 +351,59 @@ __global__ __launch_bounds__(kThreads, (GLU && MT == 4) ? 2 : 4) void hex_moe_ke
     }
   };
 
+  // partial-sum exchange of items split between workgroups (per wave, no workgroup barrier)
+  const int64_t npart_floats = G * 2 * kWaves * PF;
+  const __amdgpu_buffer_rsrc_t rp = buffer_rsrc(a.part, npart_floats * 4);
+  auto part_off = [&](int64_t gg, int which, int mt, int m) {   // byte offset of this lane's float4
+    return (int)((((gg * 2 + which) * kWaves + wave) * PF + (mt * NM + m) * kWave * 4 + lane * 4) * 4);
+  };
+  auto real_rows = [&](int b, int mt) {    // does this lane hold any real slot row?
+    const int r0 = b * BM + mt * 16 + 4 * lg;
+    return min(min(slots[r0], slots[r0 + 1]), min(slots[r0 + 2], slots[r0 + 3])) < a.num_slots;
+  };
+
   // epilogue of one item (reference order: acc * es; silu(g) * (u * es_u); * topk weight)
-  auto epilogue = [&](const Pos& p, int e) {
-    if constexpr (MT == 1) {
-      if (KS > 1) {
-        // partials pass through LDS RCH floats per lane at a time, which keeps the area small
-        // enough for two workgroups per compute unit beside the lookup tables
+  auto epilogue = [&](const Pos& p, int b, bool full, bool first) {
+    if (!full) {
+      const int64_t it = (pm0 + p.pm) * nrt + p.pn;
+      const int g_lo = owner(it * nsteps, U, G), g_hi = owner(it * nsteps + nsteps - 1, U, G);
+      const int which = first ? 0 : 1;
 #pragma unroll
-        for (int q = 0; q < NV / RCH; ++q) {
-          __syncthreads();       // the previous pass's readers of red are done
-          if (wk > 0) {
-            float* dst = red + ((wk - 1) * NWN + wn) * RCH * 64;
+      for (int mt = 0; mt < MT; ++mt) {
+        if (!real_rows(b, mt)) continue;
 #pragma unroll
-            for (int i = 0; i < RCH; ++i) dst[i * 64 + lane] = acc[0][(q * RCH + i) / 4][(q * RCH + i) % 4];
-          }
-          __syncthreads();
-          if (wk == 0) {
+        for (int m = 0; m < NM; ++m)
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[mt][m]), rp, part_off(g, which, mt, m),
+                                                 0, kCohere);
+      }
+      __builtin_amdgcn_s_waitcnt(0);     // the partial is visible device-wide before the count
+      int* cnt = a.counters + it * kWaves + wave;
+      int old = 0;
+      if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      old = __builtin_amdgcn_readlane(old, 0);
+      if (old != g_hi - g_lo) return;    // another workgroup finishes this item
+      if (lane == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // sum the parts in workgroup order
 #pragma unroll
-            for (int j = 1; j < 4; ++j) {    // k_split <= 4
-              if (j < KS) {
-                const float* src = red + ((j - 1) * NWN + wn) * RCH * 64;
+      for (int mt = 0; mt < MT; ++mt) {
+        if (!real_rows(b, mt)) continue;
 #pragma unroll
-                for (int i = 0; i < RCH; ++i) acc[0][(q * RCH + i) / 4][(q * RCH + i) % 4] += src[i * 64 + lane];
-              }
+        for (int m = 0; m < NM; ++m) {
+          f32x4 t = acc[mt][m];
+          for (int gg = g_lo; gg <= g_hi; ++gg) {
+            f32x4 v = acc[mt][m];
+            if (gg != g) {
+              const int w = (U * gg / G) / nsteps == it ? 0 : 1;
+              v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, part_off(gg, w, mt, m), 0, kCohere));
             }
+            t = gg == g_lo ? v : t + v;
           }
+          acc[mt][m] = t;
         }
       }
     }
-    if (wk != 0 || e < 0) return;
-    const int n = p.pn * BN + wn * 16 + ln;
-    if (n >= a.N) return;
-    const int b = min(p.pm, MAXBLK - 1);
+    const int nrow = p.pn * kRows + wave * 16 + ln;
+    if (nrow >= a.N) return;
     const float es0 = blk_es[b][0], es1 = blk_es[b][NM - 1];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -411,52 +413,81 @@ __global__ __launch_bounds__(kThreads, (GLU && MT == 4) ? 2 : 4) void hex_moe_ke
         const int slot = slots[row];
         if (slot >= a.num_slots) continue;
         if constexpr (GLU) {
-          const float g = acc[mt][0][r] * es0;
-          const float h = g / (1.0f + expf(-g)) * (acc[mt][1][r] * es1);
-          reinterpret_cast<uint16_t*>(a.out)[(int64_t)slot * a.s_om + n] = (uint16_t)to_bits<ADT>(h);
+          const float gt = acc[mt][0][r] * es0;
+          const float h = gt / (1.0f + expf(-gt)) * (acc[mt][1][r] * es1);
+          reinterpret_cast<uint16_t*>(a.out)[(int64_t)slot * a.s_om + nrow] = (uint16_t)to_bits<ADT>(h);
         } else {
           const float y = acc[mt][0][r] * es0 * slot_w[row];
-          reinterpret_cast<float*>(a.out)[(int64_t)slot * a.s_om + n] = y;
+          reinterpret_cast<float*>(a.out)[(int64_t)slot * a.s_om + nrow] = y;
         }
       }
   };
 
-  // ---- one pipeline over (item, chunk of D steps): loads run one chunk ahead, across item
-  // boundaries; chunks never straddle items, so control is per chunk, not per step
-  const int cpi = spw_p / D;                               // chunks per item
-  const int nchunks = nitems * cpi;
-  Stage<BITS, MT, NM> st[D];
-  Pos lp{0, pn0, 0}, cp{0, pn0, 0};
+  // ---- prologue: descriptors and the first P steps in flight, then the rest of the staging
+  Pos cp{0, (int)(item0 - pm0 * nrt), (int)(ub - item0 * nsteps)};
+  Pos lp = cp;
+  Stage<BITS, MT, NM> st[P];
+  int jl = 0;
   setup(lp);
 #pragma unroll
-  for (int d = 0; d < D; ++d) load(d, st[d]);
-  advance(lp);
-  int cur_b = -1;
-  for (int c = 0; c < nchunks; ++c) {
-    const int b = min(cp.pm, MAXBLK - 1);
-    const int e = __builtin_amdgcn_readfirstlane(blk_e[b]);
-    if (cp.sidx == 0) {
-      if (e >= 0 && (cur_b < 0 || blk_e[cur_b] != e)) {
-        __syncthreads();
-        build_table(b);
-        __syncthreads();
-        cur_b = b;
-      }
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int m = 0; m < NM; ++m) acc[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-    if (lp.sidx == 0) setup(lp);
-    const int sc = s0 + cp.sidx;
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-      if (e >= 0 && cp.sidx + d < spw && sc + d < nsteps) compute(sc + d, st[d]);
-      load(lp.sidx + d, st[d]);
-    }
-    if (cp.sidx + D == spw_p) epilogue(cp, e);
-    advance(cp);
+  for (int d = 0; d < P; ++d) {
+    if (d > 0 && lp.s == 0 && jl < n) setup(lp);
+    load(lp.s, jl < n, st[d]);
     advance(lp);
+    ++jl;
+  }
+  for (int b = tid; b < MAXBLK; b += kThreads) {
+    const int e = expert_of(b);
+#pragma unroll
+    for (int m = 0; m < NM; ++m) blk_es[b][m] = e >= 0 ? (m == 0 ? a.w0 : a.w1).expert_scale[e] : 0.f;
+  }
+  if constexpr (!GLU)
+    for (int r = tid; r < MAXBLK * BM; r += kThreads) slot_w[r] = slots[r] < a.num_slots ? a.topk_w[slots[r]] : 0.f;
+  for (int i = tid; i < MAXBLK * NM * L; i += kThreads) {
+    const int b = i / (NM * L), m = (i / L) % NM, c = i % L;
+    const int e = expert_of(b);
+    blk_lv[b][m][c] = e >= 0 ? (uint16_t)to_bits<ADT>((m == 0 ? a.w0 : a.w1).levels[(int64_t)e * L + c]) : 0;
+  }
+  // (the first step's ring write below is followed by a barrier that also publishes these)
+
+  // ---- main loop over the range's units, P per trip so the register stages stay static
+  int cur_e = -1, sa = 0;
+  bool first = true;
+  for (int j0 = 0; j0 < n; j0 += P) {
+#pragma unroll
+    for (int d = 0; d < P; ++d) {
+      const int j = j0 + d;
+      if (j < n) {
+        uint32_t* tile = ring[j & 1];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) tile[mt * 1024 + wave * 64 + lane] = st[d].ax[mt];
+        __syncthreads();                 // the tile is complete; step j - 2's readers of this stage are done
+        const int b = min(cp.pm, MAXBLK - 1);
+        const int e = __builtin_amdgcn_readfirstlane(expert_of(b));
+        if (e >= 0 && e != cur_e) {
+          build_table(b);
+          __syncthreads();
+          cur_e = e;
+        }
+        if (j == 0 || cp.s == 0) {
+          sa = cp.s;
+          first = j == 0;
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int m = 0; m < NM; ++m) acc[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        if (e >= 0) {
+          compute(cp.s, st[d], tile);
+          if (cp.s == nsteps - 1 || j == n - 1) epilogue(cp, b, sa == 0 && cp.s == nsteps - 1, first);
+        }
+        advance(cp);
+      }
+      if (lp.s == 0 && jl < n) setup(lp);
+      load(lp.s, jl < n, st[d]);
+      advance(lp);
+      ++jl;
+    }
   }
 }
 
@@ -490,22 +521,15 @@ __global__ __launch_bounds__(256) void moe_reduce_kernel(const float* __restrict
 
 // ----------------------------------------------------------------------------------- host side
 
-// Dynamic LDS for the k-split partials: one reduction pass of (k_split - 1) waves per row tile.
-template <bool GLU, int MT>
-static size_t red_bytes(int ks) {
-  return ks > 1 ? (size_t)(ks - 1) * (kWaves / ks) * red_chunk<GLU>() * kWave * sizeof(float) : 16;
-}
-
 template <int BITS, int ADT, bool GLU, int MT>
 static void launch_sb(int sb, dim3 grid, hipStream_t st, const MoeArgs& a) {
   const bool kf = (a.K / kHexBlock) % 4 == 0;     // whole 128-input steps: no tail checks
-  const size_t shm = red_bytes<GLU, MT>(a.k_split);
   const dim3 block(kThreads);
   if (sb == 1) {
-    if (kf) hipLaunchKernelGGL((hex_moe_kernel<BITS, ADT, GLU, MT, 1, true>), grid, block, shm, st, a);
-    else hipLaunchKernelGGL((hex_moe_kernel<BITS, ADT, GLU, MT, 1, false>), grid, block, shm, st, a);
+    if (kf) hipLaunchKernelGGL((hex_moe_kernel<BITS, ADT, GLU, MT, 1, true>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((hex_moe_kernel<BITS, ADT, GLU, MT, 1, false>), grid, block, 0, st, a);
   } else {   // 128-input scale blocks imply whole steps
-    hipLaunchKernelGGL((hex_moe_kernel<BITS, ADT, GLU, MT, 4, true>), grid, block, shm, st, a);
+    hipLaunchKernelGGL((hex_moe_kernel<BITS, ADT, GLU, MT, 4, true>), grid, block, 0, st, a);
   }
 }
 
@@ -529,10 +553,7 @@ static void launch_moe(int bits, int adt, int mt, int sb, dim3 grid, hipStream_t
 
 static bool aligned(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
 
-// Persistent grid: at most two workgroups per compute unit (64 KB pair tables each), never more
-// than there are (expert block, row tile) items, and enough that no workgroup's contiguous item
-// range spans more expert blocks than it stages in LDS (64 / MT).
-static dim3 persistent_grid(int64_t num_blocks, int64_t n_out, int block_n, int mt) {
+static int device_cus() {
   static int cus[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
@@ -541,11 +562,31 @@ static dim3 persistent_grid(int64_t num_blocks, int64_t n_out, int block_n, int 
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
     cus[dev] = n;
   }
-  const int64_t items = num_blocks * cdiv(n_out, block_n);
-  int64_t g = items < 2 * (int64_t)cus[dev] ? items : 2 * (int64_t)cus[dev];
+  return cus[dev];
+}
+
+// Persistent grid: one workgroup per compute unit, fewer when the plan's units (an upper bound
+// from num_blocks) would give a workgroup fewer than kMinUnits steps, and enough that no
+// workgroup's range spans more expert blocks than it stages in LDS (64 / MT).
+static int64_t moe_grid(int64_t num_blocks, int64_t n_out, int64_t n_in, int mt) {
+  const int64_t units = num_blocks * cdiv(n_out, kRows) * cdiv(cdiv(n_in, kHexBlock), 4);
+  int64_t g = cdiv(units, kMinUnits);
+  if (g > device_cus()) g = device_cus();
   const int64_t min_g = cdiv(num_blocks, kMaxBlk16 / mt - 2);
   if (g < min_g) g = min_g;
-  return dim3((unsigned)(g > 0 ? g : 1));
+  return g > 0 ? g : 1;
+}
+
+struct Workspace {
+  int64_t counter_bytes, part_bytes;
+};
+
+static Workspace workspace_layout(int64_t num_blocks, int64_t n_out, int64_t n_in, int mt, bool glu) {
+  const int64_t items = num_blocks * cdiv(n_out, kRows);
+  Workspace w;
+  w.counter_bytes = cdiv(items * kWaves * 4, 256) * 256;
+  w.part_bytes = moe_grid(num_blocks, n_out, n_in, mt) * 2 * kWaves * (int64_t)mt * (glu ? 2 : 1) * kWave * 16;
+  return w;
 }
 
 // Shared argument checks of the two fused entry points; fills the plan part of MoeArgs.
@@ -558,15 +599,13 @@ static int check_moe(const char* who, int32_t bits, int32_t adt, int64_t n_out, 
   if (!tile) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": null tile");
   if (tile->block_m != 16 && tile->block_m != 32 && tile->block_m != 64)
     return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": block_m must be 16, 32 or 64");
-  if (tile->k_split != 1 && tile->k_split != 2 && tile->k_split != 4)
-    return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": k_split must be 1, 2 or 4");
-  if (tile->block_n != 128 / tile->k_split)
-    return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": block_n must be 128 / k_split");
-  if (tile->k_split > 1 && tile->block_m != 16)
-    return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": k_split > 1 needs block_m 16");
+  if (tile->block_n != kRows || tile->k_split != 1)
+    return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": block_n must be 256 and k_split 1");
   if (n_out <= 0 || n_out > (1 << 30) || n_in > (1 << 30)) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": bad width");
   if (n_experts <= 0 || num_slots < 0 || num_blocks < 0 || num_blocks > INT32_MAX)
     return fail(BH_HEX_ERR_VALUE, std::string(who) + ": bad plan sizes");
+  if (n_experts > kMaxExperts)
+    return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": at most 1024 experts");
   if (num_blocks > 0 && (!sid || !eid || !npp || !lookup))
     return fail(BH_HEX_ERR_VALUE, std::string(who) + ": null plan pointer");
   *mt = tile->block_m / 16;
@@ -578,8 +617,21 @@ static int check_moe(const char* who, int32_t bits, int32_t adt, int64_t n_out, 
   a.num_slots = num_slots;
   a.N = (int32_t)n_out;
   a.K = (int32_t)n_in;
-  a.k_split = tile->k_split;
   (void)sb;
+  return BH_HEX_OK;
+}
+
+// Points the kernel at the caller's workspace: counters first, then the partial sums.
+static int attach_workspace(const char* who, void* ws, int64_t ws_bytes, int64_t num_blocks, int64_t n_out,
+                            int64_t n_in, int mt, bool glu, MoeArgs& a, dim3* grid) {
+  const Workspace w = workspace_layout(num_blocks, n_out, n_in, mt, glu);
+  if (!ws || ws_bytes < w.counter_bytes + w.part_bytes)
+    return fail(BH_HEX_ERR_VALUE, std::string(who) + ": workspace smaller than bh_hex_moe_workspace_bytes()");
+  if (!aligned(ws, 256)) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": workspace must be 256-byte aligned");
+  if (w.part_bytes > 0x7FFFFFFF) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": plan too large");
+  a.counters = reinterpret_cast<int*>(ws);
+  a.part = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + w.counter_bytes);
+  *grid = dim3((unsigned)moe_grid(num_blocks, n_out, n_in, mt));
   return BH_HEX_OK;
 }
 
@@ -605,7 +657,8 @@ extern "C" int bh_hex_moe_glu(const void* x, int32_t x_dtype, int64_t s_xm, void
                               const bh_hex_proj* gate, const bh_hex_proj* up, int32_t bits, int64_t n_out, int64_t n_in,
                               const int32_t* sorted_ids, const int32_t* expert_ids, int64_t num_blocks,
                               const int32_t* npp, const int32_t* lookup, int32_t n_experts, int64_t num_slots,
-                              int32_t a_div, const bh_hex_tile* tile, void* stream) {
+                              int32_t a_div, const bh_hex_tile* tile, void* workspace, int64_t workspace_bytes,
+                              void* stream) {
   const char* who = "bh_hex_moe_glu";
   MoeArgs a{};
   int mt = 0, sb = 0, words = 1;
@@ -617,7 +670,10 @@ extern "C" int bh_hex_moe_glu(const void* x, int32_t x_dtype, int64_t s_xm, void
   if (a_div <= 0) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": a_div must be positive");
   if (!x || !act) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": null activation pointer");
   if (s_xm % 8 || !aligned(x, 16)) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": x rows must be 16-byte aligned");
+  if (cdiv(num_slots, a_div) * s_xm * 2 > 0x7FFFFFFF) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": x over 2 GiB");
   if (num_blocks == 0 || num_slots == 0) return BH_HEX_OK;
+  dim3 grid;
+  if ((rc = attach_workspace(who, workspace, workspace_bytes, num_blocks, n_out, n_in, mt, true, a, &grid))) return rc;
   a.x = reinterpret_cast<const uint16_t*>(x);
   a.s_xm = s_xm;
   a.out = act;
@@ -626,7 +682,6 @@ extern "C" int bh_hex_moe_glu(const void* x, int32_t x_dtype, int64_t s_xm, void
   a.w1 = *up;
   a.a_div = a_div;
   a.scale_words = words;
-  const dim3 grid = persistent_grid(num_blocks, n_out, tile->block_n, mt);
   launch_moe<true>(bits, x_dtype, mt, sb, grid, reinterpret_cast<hipStream_t>(stream), a);
   return check_launch(who);
 }
@@ -635,7 +690,8 @@ extern "C" int bh_hex_moe_down(const void* act, int32_t act_dtype, int64_t s_am,
                                const bh_hex_proj* down, int32_t bits, int64_t n_out, int64_t n_in,
                                const int32_t* sorted_ids, const int32_t* expert_ids, int64_t num_blocks,
                                const int32_t* npp, const int32_t* lookup, int32_t n_experts, int64_t num_slots,
-                               const float* topk_w, const bh_hex_tile* tile, void* stream) {
+                               const float* topk_w, const bh_hex_tile* tile, void* workspace, int64_t workspace_bytes,
+                               void* stream) {
   const char* who = "bh_hex_moe_down";
   MoeArgs a{};
   int mt = 0, sb = 0, words = 1;
@@ -645,7 +701,10 @@ extern "C" int bh_hex_moe_down(const void* act, int32_t act_dtype, int64_t s_am,
   if ((rc = proj_setup(who, down, bits, n_in, &sb, &words))) return rc;
   if (!act || !y || !topk_w) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": null pointer");
   if (s_am % 8 || !aligned(act, 16)) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": act rows must be 16-byte aligned");
+  if (num_slots * s_am * 2 > 0x7FFFFFFF) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": act over 2 GiB");
   if (num_blocks == 0 || num_slots == 0) return BH_HEX_OK;
+  dim3 grid;
+  if ((rc = attach_workspace(who, workspace, workspace_bytes, num_blocks, n_out, n_in, mt, false, a, &grid))) return rc;
   a.x = reinterpret_cast<const uint16_t*>(act);
   a.s_xm = s_am;
   a.out = y;
@@ -655,9 +714,15 @@ extern "C" int bh_hex_moe_down(const void* act, int32_t act_dtype, int64_t s_am,
   a.topk_w = topk_w;
   a.a_div = 1;
   a.scale_words = words;
-  const dim3 grid = persistent_grid(num_blocks, n_out, tile->block_n, mt);
   launch_moe<false>(bits, act_dtype, mt, sb, grid, reinterpret_cast<hipStream_t>(stream), a);
   return check_launch(who);
+}
+
+extern "C" int64_t bh_hex_moe_workspace_bytes(int64_t num_blocks, int64_t n_out, int64_t n_in, int32_t block_m,
+                                              int32_t glu) {
+  if (num_blocks < 0 || n_out <= 0 || n_in <= 0 || (block_m != 16 && block_m != 32 && block_m != 64)) return -1;
+  const Workspace w = workspace_layout(num_blocks, n_out, n_in, block_m / 16, glu != 0);
+  return w.counter_bytes + w.part_bytes;
 }
 
 extern "C" int bh_hex_moe_reduce(const float* y, int64_t s_ym, const void* topk_ids, int32_t ids_dtype,

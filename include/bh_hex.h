@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define BH_HEX_ABI_VERSION 1
+#define BH_HEX_ABI_VERSION 2
 
 enum bh_hex_status {
   BH_HEX_OK = 0,
@@ -63,9 +63,9 @@ typedef struct bh_hex_proj {
 } bh_hex_proj;
 
 /* Tile choice of the fused kernels (the config dict of hex_moe.py:264-283, CDNA4 terms):
- * block_m slots per expert block (16, 32 or 64), k_split waves sharing one 16-row output
- * tile along the input dimension (1, 2 or 4; above 1 only with block_m 16), block_n output
- * rows per 8-wave workgroup, which must be 128 / k_split. */
+ * block_m slots per expert block (16, 32 or 64). block_n, the output rows of one work item
+ * (16 per wave of a 16-wave workgroup), must be 256; k_split must be 1 (the inputs of an item
+ * are split between workgroups by the kernels themselves). */
 typedef struct bh_hex_tile {
   int32_t block_m;
   int32_t block_n;
@@ -123,7 +123,7 @@ int bh_hex_moe_glu(const void* x, int32_t x_dtype, int64_t s_xm, void* act, int6
                    const bh_hex_proj* gate, const bh_hex_proj* up, int32_t bits, int64_t n_out, int64_t n_in,
                    const int32_t* sorted_ids, const int32_t* expert_ids, int64_t num_blocks, const int32_t* npp,
                    const int32_t* lookup, int32_t n_experts, int64_t num_slots, int32_t a_div,
-                   const bh_hex_tile* tile, void* stream);
+                   const bh_hex_tile* tile, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* The down half over one tier: y[s, o] = (es_d * sum_i act[s, i] W_d[o, i]) * topk_w[s],
  * written as float32 y [num_slots, n_out] (row stride s_ym) for the slots of every block of
@@ -132,7 +132,16 @@ int bh_hex_moe_down(const void* act, int32_t act_dtype, int64_t s_am, float* y, 
                     const bh_hex_proj* down, int32_t bits, int64_t n_out, int64_t n_in,
                     const int32_t* sorted_ids, const int32_t* expert_ids, int64_t num_blocks, const int32_t* npp,
                     const int32_t* lookup, int32_t n_experts, int64_t num_slots, const float* topk_w,
-                    const bh_hex_tile* tile, void* stream);
+                    const bh_hex_tile* tile, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Device workspace bytes bh_hex_moe_glu (glu != 0) or bh_hex_moe_down needs for a plan of
+ * num_blocks blocks of block_m slots over n_out x n_in projections, on the current device
+ * (-1 for bad arguments). The workspace (256-byte aligned) must be zero-filled before its first
+ * use; every call leaves it zero-filled again, so it can be kept and reused. Calls that share a
+ * workspace must not overlap in time (one stream, or ordered streams). No counterpart in the
+ * reference, whose Triton kernels need none: it holds per-item arrival counters and the partial
+ * sums of items whose inputs are split between workgroups. */
+int64_t bh_hex_moe_workspace_bytes(int64_t num_blocks, int64_t n_out, int64_t n_in, int32_t block_m, int32_t glu);
 
 /* out[t, h] = sum_j y[t * k + j, h] over the token's k slots, in float32, rounded once to
  * out_dtype (F32, BF16 or F16); slots whose id (topk_ids, I32 or I64) is outside

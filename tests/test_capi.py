@@ -44,6 +44,17 @@ def test_align_max_blocks_formula():
     assert lib.bh_hex_align_max_blocks(4, 4, 0) == -1
 
 
+def test_workspace_bytes():
+    lib = _lib.load()
+    assert lib.bh_hex_moe_workspace_bytes(-1, 64, 64, 16, 1) == -1
+    assert lib.bh_hex_moe_workspace_bytes(4, 64, 64, 24, 1) == -1
+    glu = lib.bh_hex_moe_workspace_bytes(104, 768, 2048, 16, 1)
+    down = lib.bh_hex_moe_workspace_bytes(104, 2048, 768, 16, 0)
+    assert glu > 0 and down > 0 and glu % 256 == 0 and down % 256 == 0
+    # counters (items x 16 waves) plus partial tiles, which grow with block_m
+    assert lib.bh_hex_moe_workspace_bytes(104, 768, 2048, 64, 1) > glu
+
+
 def _status(rc, code, pattern):
     lib = _lib.load()
     assert rc == code
@@ -67,18 +78,19 @@ def test_host_side_errors():
     bad = _lib.HexProj(16, 16, 16, 16, 0, 0, 0, 0, 48)
     _status(lib.bh_hex_dequant(ctypes.byref(bad), 4, 1, 1, 96, None, 16, _lib.F32, 0, 96, 0, 0, None),
             _lib.ERR_VALUE, "scale block")
-    tile = _lib.HexTile(16, 32, 1)
-    _status(lib.bh_hex_moe_glu(16, _lib.BF16, 64, 16, 64, ctypes.byref(w), ctypes.byref(w), 4, 64, 64,
-                               16, 16, 1, 16, 16, 4, 4, 1, ctypes.byref(tile), None),
-            _lib.ERR_UNSUPPORTED, "block_n")
-    tile = _lib.HexTile(32, 64, 2)
-    _status(lib.bh_hex_moe_glu(16, _lib.BF16, 64, 16, 64, ctypes.byref(w), ctypes.byref(w), 4, 64, 64,
-                               16, 16, 1, 16, 16, 4, 4, 1, ctypes.byref(tile), None),
-            _lib.ERR_UNSUPPORTED, "block_m 16")
-    tile = _lib.HexTile(16, 128, 1)
+    for bad in (_lib.HexTile(16, 32, 1), _lib.HexTile(32, 256, 2)):
+        _status(lib.bh_hex_moe_glu(16, _lib.BF16, 64, 16, 64, ctypes.byref(w), ctypes.byref(w), 4, 64, 64,
+                                   16, 16, 1, 16, 16, 4, 4, 1, ctypes.byref(bad), None, 0, None),
+                _lib.ERR_UNSUPPORTED, "block_n must be 256")
+    tile = _lib.HexTile(16, 256, 1)
     _status(lib.bh_hex_moe_glu(16, _lib.F32, 64, 16, 64, ctypes.byref(w), ctypes.byref(w), 4, 64, 64,
-                               16, 16, 1, 16, 16, 4, 4, 1, ctypes.byref(tile), None),
+                               16, 16, 1, 16, 16, 4, 4, 1, ctypes.byref(tile), None, 0, None),
             _lib.ERR_UNSUPPORTED, "BF16 or F16")
+    # a plan with blocks needs the workspace (checked before anything reaches the device)
+    w32 = _lib.HexProj(16, 16, 16, 16, 0, 4, 0, 1, 32)
+    _status(lib.bh_hex_moe_glu(16, _lib.BF16, 64, 16, 64, ctypes.byref(w32), ctypes.byref(w32), 4, 64, 64,
+                               16, 16, 1, 16, 16, 4, 4, 1, ctypes.byref(tile), None, 0, None),
+            _lib.ERR_VALUE, "workspace")
     _status(lib.bh_hex_moe_reduce(16, 6, 16, _lib.I64, 4, 2, 2, 6, 16, _lib.BF16, 6, None),
             _lib.ERR_UNSUPPORTED, "H % 4")
 

@@ -52,19 +52,16 @@ def test_block_from_shapes_128():
 
 
 def test_default_config_and_env(monkeypatch):
-    c = hm.default_config(8, 768, 2048, True, 96)          # T=1 decode: 8 expert blocks
-    assert c["BLOCK_M"] == 16 and c["K_SPLIT"] == 4 and c["BLOCK_N"] == 32
-    c = hm.default_config(128, 768, 2048, True, 96)        # T=16
-    assert c["BLOCK_M"] == 16 and c["K_SPLIT"] == 2 and c["BLOCK_N"] == 64
-    c = hm.default_config(32768, 2048, 768, False, 96)     # prefill: many slots per expert
-    assert c["BLOCK_M"] == 64
-    assert hm.default_config(32768, 768, 2048, True, 96)["BLOCK_M"] == 32
-    monkeypatch.setenv("BLACKHOLE_HEX_TILES", "16,64")
-    assert hm.default_config(8, 768, 2048, True, 96) == {"BLOCK_M": 16, "BLOCK_N": 64, "K_SPLIT": 2}
+    assert hm.default_config(8, 768, 2048, True, 96) == {"BLOCK_M": 16, "BLOCK_N": 256}    # T=1 decode
+    assert hm.default_config(128, 768, 2048, True, 96)["BLOCK_M"] == 16                    # T=16
+    assert hm.default_config(32768, 2048, 768, False, 96)["BLOCK_M"] == 64                 # prefill
+    assert hm.default_config(3000, 768, 2048, True, 96)["BLOCK_M"] == 32
+    monkeypatch.setenv("BLACKHOLE_HEX_TILES", "64")
+    assert hm.default_config(8, 768, 2048, True, 96) == {"BLOCK_M": 64, "BLOCK_N": 256}
     # the reference's own config keys map onto the tile
-    assert hm._tile_from({"BLOCK_M": 16, "BLOCK_N": 32, "BLOCK_K": 32, "num_warps": 4, "num_stages": 1}) == (16, 4)
-    assert hm._tile_from({"BLOCK_M": 128, "BLOCK_N": 128}) == (64, 1)
-    assert hm._tile_from({"BLOCK_M": 32, "BLOCK_N": 32}) == (32, 1)     # input split: 16-slot blocks only
+    assert hm._tile_from({"BLOCK_M": 16, "BLOCK_N": 32, "BLOCK_K": 32, "num_warps": 4, "num_stages": 1}) == 16
+    assert hm._tile_from({"BLOCK_M": 128, "BLOCK_N": 128}) == 64
+    assert hm._tile_from({"BLOCK_M": 24}) == 32
 
 
 def test_kernels_refuse_cpu_tensors():
