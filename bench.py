@@ -1,7 +1,8 @@
 """HEX MoE layer benchmark on one MI355X.
 
     python bench.py [--gpus 1] [--steps 400] [--warmup 40] [--config 2] [--tokens 16]
-                    [--no-sweep] [--no-cpu-baseline]
+                    [--no-sweep] [--no-cpu-baseline] [--copy-calibration]
+    python bench.py --rocprof-summary DIR [DIR ...]     (summarise rocprofv3 CSV output)
 
 A step is one HEX MoE layer call (hex_moe through the fused HIP kernels: slot plan, gate/up +
 SiLU, down + top-k weight, k-slot sum) on one batch of synthetic tokens with inputs resident
@@ -205,21 +206,26 @@ def run_layer(cfg, copies, T, steps, warmup, block, breakdown=True):
     x, w, ids, logits = make_inputs(cfg, T, dev)
     n = len(copies)
 
-    def layers():
-        for tiers in copies:
-            hm.hex_moe(x, w, ids, tiers, path="fused")
+    def layers(m):
+        def fn():
+            for tiers in copies[:m]:
+                hm.hex_moe(x, w, ids, tiers, path="fused")
+        return fn
 
-    g = graph_of(layers)
-    reps = max(1, -(-steps // n))
+    g = graph_of(layers(n))
+    rem = steps % n                          # exactly `steps` layer calls: full replays + one partial
+    g_rem = graph_of(layers(rem)) if rem else None
     for _ in range(max(1, -(-warmup // n))):
         g.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(reps):
+    for _ in range(steps // n):
         g.replay()
+    if g_rem is not None:
+        g_rem.replay()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    calls = reps * n
+    calls = steps
     ms = elapsed * 1e3 / calls
     total, glu_b, used = layer_bytes(cfg, copies[0], ids, block, T)
     S = T * cfg["k"]
@@ -229,20 +235,25 @@ def run_layer(cfg, copies, T, steps, warmup, block, breakdown=True):
            "hbm_frac": total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
            "mfma_frac": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, "glu_bytes": glu_b}
     if breakdown:
-        out["kernels"] = kernel_breakdown(cfg, copies, x, w, ids, max(5, reps // 2))
+        out["kernels"] = kernel_breakdown(cfg, copies, x, w, ids, max(5, steps // (2 * n)))
     return out, (x, w, ids, logits)
 
 
-def cpu_baseline(cfg, tiers, x, w, ids, runs=3):
-    """The CPU oracle (numpy float32 restatement of hex_ref.moe_reference) on one layer call of
-    the same workload, one BLAS thread; median of `runs` calls."""
+def cpu_threads() -> int:
+    """Host threads this process may use: OMP_NUM_THREADS when set (the GPU box's CPU share),
+    else the affinity mask."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return int(env) if env.isdigit() and int(env) > 0 else len(os.sched_getaffinity(0))
+
+
+def cpu_baseline(cfg, tiers, x, w, ids, budget_s=12.0):
+    """The CPU oracle (numpy float32 restatement of hex_ref.moe_reference: dequant every routed
+    expert, per-expert matmuls) on one layer call of the same workload with all host threads the
+    process may use; calls repeat until budget_s of CPU work (at least 3), median reported."""
     import numpy as np
 
     from oracle import hex_oracle as O
-    try:
-        from threadpoolctl import threadpool_limits
-    except ImportError:                                  # pragma: no cover
-        threadpool_limits = None
+    from threadpoolctl import threadpool_limits
     ref = []
     for t in tiers:
         parts = {}
@@ -252,19 +263,15 @@ def cpu_baseline(cfg, tiers, x, w, ids, runs=3):
                            "expert_scale": p["expert_scale"].cpu().numpy(), "levels": p["levels"].cpu().numpy()}
         ref.append({"bits": t.bits, "experts": t._experts_host.numpy(), **parts})
     xn, wn, idn = x.float().cpu().numpy(), w.cpu().numpy(), ids.cpu().numpy()
+    threads = cpu_threads()
     times = []
-    ctx = threadpool_limits(1) if threadpool_limits else None
-    try:
-        if ctx:
-            ctx.__enter__()
-        for _ in range(runs):
+    with threadpool_limits(threads):
+        t_start = time.perf_counter()
+        while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 20):
             t0 = time.perf_counter()
             O.moe_reference(xn, wn, idn, ref, "bf16")
             times.append(time.perf_counter() - t0)
-            log(f"  cpu baseline call: {times[-1]:.2f} s")
-    finally:
-        if ctx:
-            ctx.__exit__(None, None, None)
+            log(f"  cpu baseline call {len(times)}: {times[-1]:.2f} s")
     med = float(np.median(times))
     model = "unknown CPU"
     try:
@@ -275,9 +282,83 @@ def cpu_baseline(cfg, tiers, x, w, ids, runs=3):
     except OSError:
         pass
     T = ids.shape[0]
-    return {"value": T / med, "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"{runs} calls of the oracle moe_reference (numpy float32, 1 BLAS thread) on the benchmark "
-                      f"layer at T={T}, median {med:.2f} s per call, on {model}"}
+    return {"value": T / med, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{len(times)} calls of the oracle moe_reference (numpy float32, {threads} BLAS threads) on "
+                      f"the benchmark layer at T={T} ({sum(times):.1f} s of CPU work), median {med:.3f} s per call, "
+                      f"on {model}"}
+
+
+# ----------------------------------------------------------------------------- rocprofv3 summaries
+
+PROFILES = ROOT / "profiles"
+TRAFFIC_FILE = PROFILES / "hex_moe_glu_config2_T16_traffic.json"
+GLU_KERNEL = "hex_moe_kernel<4, 1, true, 1, 4, true>"      # gate/up, 4-bit, bf16, block_m 16, 128-input scales
+COPY_BYTES = 2 * (128 << 20) * 2                             # the calibration kernel: 256 MiB read + 256 MiB written
+
+
+def _csv_rows(d: str, suffix: str):
+    import csv
+    import glob
+    for f in sorted(glob.glob(os.path.join(d, "**", "*" + suffix), recursive=True)):
+        with open(f) as fh:
+            yield from csv.DictReader(fh)
+
+
+def _short(name: str) -> str:
+    name = name.replace("void ", "").split("(")[0]
+    return name.replace("bh::", "")[:110]
+
+
+def rocprof_summary(dirs: list[str]) -> str:
+    """Text summary of rocprofv3 CSV output directories: per-kernel dispatch statistics from a
+    --kernel-trace --stats run, mean counter values per dispatch from --pmc runs, and, when a
+    FETCH_SIZE and a WRITE_SIZE run of the --copy-calibration bench are both given, the gate/up
+    kernel's HBM traffic per launch scaled by what the same counters read for the known-size copy
+    (written to TRAFFIC_FILE)."""
+    out, counters = [], {}
+    for d in dirs:
+        stats = list(_csv_rows(d, "kernel_stats.csv"))
+        if stats:
+            out.append(f"## kernel statistics ({d})")
+            out.append(f"{'kernel':<112} {'calls':>6} {'avg_us':>9} {'min_us':>9} {'max_us':>9} {'pct':>6}")
+            for r in sorted(stats, key=lambda r: -float(r["TotalDurationNs"]))[:16]:
+                out.append(f"{_short(r['Name']):<112} {int(r['Calls']):>6} {float(r['AverageNs']) / 1e3:>9.2f} "
+                           f"{float(r['MinNs']) / 1e3:>9.2f} {float(r['MaxNs']) / 1e3:>9.2f} "
+                           f"{float(r['Percentage']):>6.2f}")
+        rows = list(_csv_rows(d, "counter_collection.csv"))
+        if rows:
+            agg: dict = {}
+            for r in rows:
+                key = (_short(r["Kernel_Name"]), r["Counter_Name"])
+                agg.setdefault(key, []).append(float(r["Counter_Value"]))
+            out.append(f"## counters, mean per dispatch ({d})")
+            for (k, c), v in sorted(agg.items()):
+                if "hex_moe" in k or "align_kernel" in k or "moe_reduce" in k or "bitwise_not" in k:
+                    out.append(f"{k:<112} {c:<12} {sum(v) / len(v):>14.1f}  (n={len(v)})")
+                counters.setdefault(c, {})[k] = v
+    if "FETCH_SIZE" in counters and "WRITE_SIZE" in counters:
+        def kernel(c, pred):
+            cand = {k: v for k, v in counters[c].items() if pred(k)}
+            return max(cand.items(), key=lambda kv: sum(kv[1]) / len(kv[1])) if cand else (None, [])
+        ck, cf = kernel("FETCH_SIZE", lambda k: "bitwise_not" in k)
+        _, cw = kernel("WRITE_SIZE", lambda k: k == ck)
+        gk, gf = kernel("FETCH_SIZE", lambda k: GLU_KERNEL in k)
+        _, gw = kernel("WRITE_SIZE", lambda k: GLU_KERNEL in k)
+        if ck and gk:
+            half = COPY_BYTES // 2                           # bytes the calibration kernel reads, and writes
+            f_scale = half / (sum(cf) / len(cf) * 1024)
+            w_scale = half / (sum(cw) / len(cw) * 1024)
+            fetch = sum(gf) / len(gf) * 1024 * f_scale
+            write = sum(gw) / len(gw) * 1024 * w_scale
+            res = {"kernel": gk, "fetch_bytes": fetch, "write_bytes": write, "traffic_bytes": fetch + write,
+                   "calibration_kernel": ck, "calibration_fetch_kib": sum(cf) / len(cf),
+                   "calibration_write_kib": sum(cw) / len(cw), "calibration_bytes_each_way": half,
+                   "fetch_scale": f_scale, "write_scale": w_scale, "dispatches": len(gf)}
+            out.append("## HBM traffic of the gate/up kernel per launch (counter KiB x 1024 x calibration scale)")
+            out.append(json.dumps(res, indent=1))
+            PROFILES.mkdir(exist_ok=True)
+            TRAFFIC_FILE.write_text(json.dumps(res) + "\n")
+    return "\n".join(out) + "\n"
 
 
 def main(argv=None) -> int:
@@ -292,9 +373,14 @@ def main(argv=None) -> int:
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
-                    help="also run a 256 MiB device-to-device copy (the known-size kernel that scales "
-                         "rocprofv3 FETCH_SIZE / WRITE_SIZE into bytes)")
+                    help="also run bitwise_not over 128 Mi int16 elements, 3 times (the known-size kernel that "
+                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE into bytes)")
+    ap.add_argument("--rocprof-summary", nargs="+", metavar="DIR",
+                    help="summarise rocprofv3 CSV output directories and exit (no GPU work)")
     a = ap.parse_args(argv)
+    if a.rocprof_summary:
+        print(rocprof_summary(a.rocprof_summary), end="")
+        return 0
     if a.gpus != 1:
         print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for --gpus {a.gpus})",
               file=sys.stderr)
@@ -317,9 +403,14 @@ def main(argv=None) -> int:
 
     k = head["kernels"]
     glu_gbs = head["glu_bytes"] / (k["glu_us"] * 1e-6) / 1e9
+    traffic, traffic_src = None, None
+    if a.config == 2 and T == 16 and a.block == 128 and TRAFFIC_FILE.exists():
+        traffic = json.loads(TRAFFIC_FILE.read_text())["traffic_bytes"]
+        traffic_src = str(TRAFFIC_FILE.relative_to(ROOT))
     roofline = {"bound": "hbm", "achieved": glu_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": glu_gbs / HBM_PEAK_GBS, "traffic": None, "kernel": "hex_moe_kernel (gate/up, SwiGLU)",
-                "algorithmic_bytes_per_launch": head["glu_bytes"], "avg_launch_us": k["glu_us"]}
+                "frac": glu_gbs / HBM_PEAK_GBS, "traffic": traffic, "traffic_source": traffic_src,
+                "kernel": f"{GLU_KERNEL} (gate/up + SiLU)", "algorithmic_bytes_per_launch": head["glu_bytes"],
+                "avg_launch_us": k["glu_us"]}
 
     sweep = {}
     if not a.no_sweep and a.config == 2:
@@ -340,12 +431,12 @@ def main(argv=None) -> int:
         torch.cuda.empty_cache()
 
     if a.copy_calibration:
-        src = torch.empty(128 << 20, dtype=torch.bfloat16, device=dev).normal_()
+        src = torch.empty(128 << 20, dtype=torch.int16, device=dev).random_()
         dst = torch.empty_like(src)
         for _ in range(3):
-            dst.copy_(src)
+            torch.bitwise_not(src, out=dst)  # a kernel used nowhere else: 256 MiB in, 256 MiB out
         torch.cuda.synchronize()
-        log(f"  copy calibration: 3 x {src.numel() * 2} bytes read and written")
+        log(f"  copy calibration: 3 x ({src.numel() * 2} bytes read + {dst.numel() * 2} written)")
         del src, dst
 
     cpu = None
