@@ -188,21 +188,26 @@ def default_config(slots: int, n_out: int, n_in: int, glu: bool, n_experts: int 
 _WORKSPACES: dict = {}
 
 
-def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Zero-filled device workspace of at least nbytes for the fused kernels on the current
-    stream. The kernels leave it zero-filled, so it is kept per (device, stream) and grown when
-    needed; one stream's calls run in order, so they never share it concurrently. Inside graph
-    capture a missing or small workspace is allocated in the graph's pool (zeroed by a captured
-    fill on every replay) and not kept."""
-    stream = torch.cuda.current_stream(device)
-    key = (device.index, stream.cuda_stream)
-    ws = _WORKSPACES.get(key)
-    if ws is not None and ws.numel() >= nbytes:
-        return ws
-    ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-    if not torch.cuda.is_current_stream_capturing():
-        _WORKSPACES[key] = ws
-    return ws
+def _workspace(device: torch.device, block_m: int, num_blocks: int, n_out: int, n_in: int, glu: bool):
+    """(counters, partials) for one fused launch on the current stream. The kernels leave the
+    int32 counters at zero, so both buffers are kept per (device, stream) and shared by every
+    call there (one stream runs its calls in order), grown when a call needs more. Inside graph
+    capture a missing or small workspace is allocated in the graph's pool (the counters zeroed
+    by a captured fill on every replay) and not kept."""
+    lib = _lib.load()
+    nc, npart = _lib.ctypes.c_int64(), _lib.ctypes.c_int64()
+    _lib.check(lib.bh_hex_moe_workspace(num_blocks, n_out, n_in, block_m, int(glu), _lib.ctypes.byref(nc),
+                                        _lib.ctypes.byref(npart)), "bh_hex_moe_workspace")
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    cnt, part = _WORKSPACES.get(key, (None, None))
+    keep = not torch.cuda.is_current_stream_capturing()
+    if cnt is None or cnt.numel() < nc.value:
+        cnt = torch.zeros(max(nc.value, 1 << 16), dtype=torch.int32, device=device)
+    if part is None or part.numel() < npart.value:
+        part = torch.empty(max(npart.value, 1 << 16), dtype=torch.float32, device=device)
+    if keep:
+        _WORKSPACES[key] = (cnt, part)
+    return cnt, part
 
 
 def _launch_glu(x, act, t: HexTier, sid, eid, npp, S, a_div, bm):
@@ -211,13 +216,12 @@ def _launch_glu(x, act, t: HexTier, sid, eid, npp, S, a_div, bm):
     n_in = _n_in(t.gate_proj, t.bits)
     assert x.shape[1] == n_in, f"input width {x.shape[1]} != HEX width {n_in}"
     tile = _lib.HexTile(bm, 256, 1)
-    nbytes = lib.bh_hex_moe_workspace_bytes(eid.numel(), n_out, n_in, bm, 1)
-    ws = _workspace(x.device, nbytes)
+    cnt, part = _workspace(x.device, bm, eid.numel(), n_out, n_in, True)
     _lib.check(lib.bh_hex_moe_glu(
         x.data_ptr(), _lib.dtype_code(x.dtype), x.stride(0), act.data_ptr(), act.stride(0),
         t.struct("gate_proj"), t.struct("up_proj"), t.bits, n_out, n_in,
         sid.data_ptr(), eid.data_ptr(), eid.numel(), npp.data_ptr(), t.lookup.data_ptr(), t.lookup.numel(), S, a_div,
-        tile, ws.data_ptr(), ws.numel(), _lib.stream_of(x)), "bh_hex_moe_glu")
+        tile, cnt.data_ptr(), cnt.numel(), part.data_ptr(), part.numel(), _lib.stream_of(x)), "bh_hex_moe_glu")
 
 
 def _launch_down(act, y, t: HexTier, sid, eid, npp, S, w, bm):
@@ -226,13 +230,13 @@ def _launch_down(act, y, t: HexTier, sid, eid, npp, S, w, bm):
     n_in = _n_in(t.down_proj, t.bits)
     assert act.shape[1] == n_in, f"input width {act.shape[1]} != HEX width {n_in}"
     tile = _lib.HexTile(bm, 256, 1)
-    nbytes = lib.bh_hex_moe_workspace_bytes(eid.numel(), n_out, n_in, bm, 0)
-    ws = _workspace(act.device, nbytes)
+    cnt, part = _workspace(act.device, bm, eid.numel(), n_out, n_in, False)
     _lib.check(lib.bh_hex_moe_down(
         act.data_ptr(), _lib.dtype_code(act.dtype), act.stride(0), y.data_ptr(), y.stride(0),
         t.struct("down_proj"), t.bits, n_out, n_in,
         sid.data_ptr(), eid.data_ptr(), eid.numel(), npp.data_ptr(), t.lookup.data_ptr(), t.lookup.numel(), S,
-        w.data_ptr(), tile, ws.data_ptr(), ws.numel(), _lib.stream_of(act)), "bh_hex_moe_down")
+        w.data_ptr(), tile, cnt.data_ptr(), cnt.numel(), part.data_ptr(), part.numel(), _lib.stream_of(act)),
+        "bh_hex_moe_down")
 
 
 def _covers_all(tiers: list[HexTier]) -> bool:

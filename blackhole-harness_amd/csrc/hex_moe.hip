@@ -53,9 +53,9 @@ struct MoeArgs {
   int32_t n_experts;
   int32_t a_div;
   int32_t N, K;
-  int32_t scale_words;   // block_scale rows allow 32-bit loads of 4 scales
+  int32_t scale_words;   // block_scale rows allow one load of a unit's scales (8 or 2 bytes)
   float* part;           // workspace: partial sums of items split between workgroups
-  int* counters;         // workspace: arrivals per (item, wave), zero between calls
+  int32_t* counters;     // workspace: arrivals per (item, wave), zero between calls
 };
 
 // Four fp8 scales (one byte each) -> float, by the conversion instruction; a wave holding a
@@ -93,23 +93,22 @@ __device__ __forceinline__ u32x4 lookup8(uint32_t f, uint32_t cb, const uint32_t
   return b;
 }
 
-template <int BITS, int MT, int NM>
+// One unit's loads of one wave: two 128-input steps.
+template <int BITS, int MT, int NM, int SB>
 struct Stage {
-  uint32_t w[NM][4];     // 4-bit: the block's 4 words; 3-bit: its 3 words
-  uint32_t sc[NM];       // block scales: 4 bytes (one per MFMA) or 1 byte (128-input block)
-  uint32_t ax[MT];       // this lane's dword of the step's activation tile (shared through LDS)
+  uint32_t w[NM][2][4];  // per step, the lane's 32-input block (4-bit: 4 words; 3-bit: 3)
+  uint32_t sc[NM][SB == 1 ? 2 : 1];   // fp8 block scales of the row: 8 bytes (B = 32) or 2 (B = 128)
 };
 
-// Buffer resources and per-lane byte offsets of one work item (expert block x row tile). Each
-// resource spans one expert's matrix (or the activations), so loads past its end return zero
-// instead of faulting; rows past the matrix and padding slots read data whose results are
-// never stored. The step offset goes in the scalar soffset, so a step costs no address math.
-template <int MT, int NM>
+// Buffer resources and per-lane byte offsets of the weight stream's current item. Each
+// resource spans one expert's matrix, so loads past its end return zero instead of faulting;
+// rows past the matrix read out of range (nothing fetched) and are never stored. The unit
+// offset goes in the scalar soffset, so a unit costs no vector address math.
+template <int NM>
 struct ItemRes {
   __amdgpu_buffer_rsrc_t rw[NM];   // packed index words of the item's expert
   __amdgpu_buffer_rsrc_t rb[NM];   // its fp8 block scales
-  int vw[NM], vb[NM];              // lane offsets: row n, block 4 s + lane / 16
-  int vx[MT];                      // lane offsets into the activations: its dword of the tile
+  int vw[NM], vb[NM];              // lane offsets: row n, block lane / 16 of the unit
 };
 
 constexpr int kRsrcWord3 = 0x00020000;   // raw buffer, 32-bit data format (gfx9 family)
@@ -128,15 +127,18 @@ constexpr int kMaxExperts = 1024;        // global expert ids the tier lookup ma
 constexpr int kThreads = 1024;           // 16 waves, one workgroup per compute unit
 constexpr int kWaves = kThreads / kWave;
 constexpr int kRows = 16 * kWaves;       // output rows of one work item: 16 per wave
-constexpr int kMinUnits = 4;             // steps per workgroup below which the grid shrinks
+constexpr int kUnitIn = 256;             // inputs per unit: two 128-input steps
+constexpr int kMinUnits = 2;             // units per workgroup below which the grid shrinks
 
-// Prefetch depth P: steps whose weights are in flight per wave (registers) ahead of the math.
+// Units per trip P: the weight loads of P units are in flight per wave ahead of the math, and
+// the activation tiles of the next P units are fetched one trip ahead; one workgroup barrier
+// per trip publishes them.
 template <int MT, bool GLU>
-constexpr int depth() { return GLU ? (MT == 1 ? 3 : (MT == 2 ? 2 : 1)) : (MT == 1 ? 4 : (MT == 2 ? 3 : 2)); }
+constexpr int trip() { return GLU ? (MT == 1 ? 2 : 1) : (MT == 4 ? 1 : 2); }
 
 constexpr int kOOR = 0x7FFF0000;   // byte offset past every resource: loads return zero, fetch nothing
 
-// Position of a unit: block (relative to the range's first), row tile, step.
+// Position of a unit: block (relative to the range's first), row tile, unit within the item.
 struct Pos {
   int pm, pn, s;
 };
@@ -146,7 +148,7 @@ template <int MT, int NM>
 constexpr int part_floats() { return MT * NM * kWave * 4; }
 
 // Work decomposition shared by the host (grid, workspace) and the kernel: units are
-// (expert block, 256-row tile, 128-input step) in that order; workgroup g takes units
+// (expert block, 256-row tile, 256-input unit) in that order; workgroup g takes units
 // [U g / G, U (g + 1) / G). An item (block, row tile) split between workgroups is summed by the
 // last of them to finish, in workgroup order, from partials in the workspace.
 __device__ __forceinline__ int owner(int64_t u, int64_t U, int64_t G) {
@@ -159,37 +161,39 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
   constexpr int NPAIR = 1 << (2 * BITS);
   constexpr int NM = GLU ? 2 : 1;
   constexpr int BM = 16 * MT;
-  constexpr int P = depth<MT, GLU>();
+  constexpr int P = trip<MT, GLU>();
   constexpr int MAXBLK = kMaxBlk16 / MT;
   constexpr int PF = part_floats<MT, NM>();
+  constexpr int TILE = MT * 1024;               // dwords of one step's activation tile
   // Everything a unit needs besides its streamed weights and activations is staged in LDS at
-  // the start; the activation tile of each step goes through a two-stage LDS ring, loaded once
-  // per workgroup (a dword per lane) and read by all 16 waves.
+  // the start. The activation tiles of a trip (P units x 2 steps) go through a two-trip ring:
+  // fetched once per workgroup, a dword per lane per tile, and read by all 16 waves.
   __shared__ __align__(16) uint32_t tab[NPAIR * 64];
-  __shared__ __align__(16) uint32_t ring[2][MT * 1024];
+  __shared__ __align__(16) uint32_t ring[2][P * 2 * TILE];
   __shared__ int lut[kMaxExperts];                                 // the tier lookup
   __shared__ int slots[MAXBLK * BM];                               // slot rows of the range's blocks
   __shared__ float slot_w[GLU ? 1 : MAXBLK * BM];                  // their top-k weights (down)
   __shared__ int blk_g[MAXBLK];                                    // global expert of each block
+  __shared__ int blk_e[MAXBLK];                                    // its tier-local expert, -1 for none
   __shared__ float blk_es[MAXBLK][NM];                             // expert scales
   __shared__ uint16_t blk_lv[MAXBLK][NM][L];                       // levels in the activation dtype
 
   const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, lg = lane >> 4;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: steps and row tiles stay scalar
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: units and row tiles stay scalar
   const int nrt = (a.N + kRows - 1) / kRows;
   const int nb32 = a.K / kHexBlock;
-  const int nsteps = (nb32 + 3) / 4;
+  const int nun = (nb32 + 7) / 8;                              // units per item
 
   // ---- this workgroup's contiguous range of units over the used blocks
   const int64_t used = (int64_t)a.npp[0] / BM;
-  const int64_t U = used * nrt * nsteps;
+  const int64_t U = used * nrt * nun;
   const int64_t G = min((int64_t)gridDim.x, U), g = blockIdx.x;   // no workgroup has an empty range
   if (g >= G) return;
   const int64_t ub = U * g / G, ue = U * (g + 1) / G;
   const int n = (int)(ue - ub);
-  const int64_t item0 = ub / nsteps;
+  const int64_t item0 = ub / nun, item1 = (ue - 1) / nun;
   const int64_t pm0 = item0 / nrt;
-  const int nblk = min((int)((ue - 1) / nsteps / nrt - pm0 + 1), MAXBLK);
+  const int nblk = min((int)(item1 / nrt - pm0 + 1), MAXBLK);
 
   // ---- stage the plan: tier lookup, block experts, slot rows
   for (int i = tid; i < a.n_experts; i += kThreads) lut[i] = a.lookup[i];
@@ -210,7 +214,7 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
     cb[0] = lane * 4u;
   }
   auto advance = [&](Pos& p) {
-    if (++p.s == nsteps) {
+    if (++p.s == nun) {
       p.s = 0;
       if (++p.pn == nrt) {
         p.pn = 0;
@@ -219,14 +223,10 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
     }
   };
 
-  // ---- load stream: buffer loads, per-item descriptors, the step in soffset
-  ItemRes<MT, NM> R;
-  const int x_rows = (int)((a.num_slots + a.a_div - 1) / a.a_div);
-  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(a.x, (int64_t)x_rows * a.s_xm * 2);
-  // this lane's dword of a step's activation tile: wave w, lane l -> slot l / 4 of the tile,
-  // inputs 32 (w / 4) + 8 (w % 4) + 2 (l % 4) of the step (the fragment layout the MFMA reads)
-  const int xcol = (wave >> 2) * 64 + (wave & 3) * 16 + (lane & 3) * 4;
-  constexpr int WSTEP = 4 * BITS * 4;          // bytes of 4 blocks of one row
+  // ---- weight stream: buffer loads, per-item descriptors, the unit in soffset
+  ItemRes<NM> R;
+  constexpr int BLKB = BITS * 4;               // bytes of one 32-input block of one row
+  constexpr int USTEP = 8 * BLKB;              // bytes of one unit of one row
   auto setup = [&](const Pos& p) {
     const int b = min(p.pm, MAXBLK - 1);
     const int e = __builtin_amdgcn_readfirstlane(expert_of(b));   // uniform: keeps descriptors scalar
@@ -238,102 +238,151 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
       const bh_hex_proj& w = m == 0 ? a.w0 : a.w1;
       R.rw[m] = buffer_rsrc(w.idx + ee * w.s_ie, (int64_t)a.N * w.s_in * 4);
       R.rb[m] = buffer_rsrc(w.block_scale + ee * w.s_be, (int64_t)a.N * w.s_bn);
-      R.vw[m] = rv ? (int)(nrow * w.s_in * 4) + lg * (BITS * 4) : kOOR;
+      R.vw[m] = rv ? (int)(nrow * w.s_in * 4) + lg * BLKB : kOOR;
       R.vb[m] = rv ? (int)(nrow * w.s_bn) : kOOR;
     }
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {                // padding slots fetch nothing
-      const int slot = slots[b * BM + mt * 16 + (lane >> 2)];
-      R.vx[mt] = (e >= 0 && slot < a.num_slots) ? (int)((int64_t)(slot / a.a_div) * a.s_xm * 2) + xcol : kOOR;
-    }
   };
-  // loads of step s of the current descriptors; dummy steps (past the range) read out of range
-  auto load = [&](int s_, bool real, Stage<BITS, MT, NM>& st) {
+  // loads of unit s of the current descriptors; dummy units (past the range) read out of range
+  auto load = [&](int s_, bool real, Stage<BITS, MT, NM, SB>& st) {
     const int s = __builtin_amdgcn_readfirstlane(real ? s_ : 0);
-    const int ws = real ? s * WSTEP : kOOR, bs1 = real ? 4 * s : kOOR, bs4 = real ? s : kOOR;
-    const int xs = real ? s * 256 : kOOR;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) st.ax[mt] = __builtin_amdgcn_raw_buffer_load_b32(rx, R.vx[mt], xs, 0);
+    const int ws = real ? s * USTEP : kOOR;
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
-      if constexpr (BITS == 4) {
-        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(R.rw[m], R.vw[m], ws, 0);
-        st.w[m][0] = v[0]; st.w[m][1] = v[1]; st.w[m][2] = v[2]; st.w[m][3] = v[3];
-      } else {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b96(R.rw[m], R.vw[m], ws, 0);
-        st.w[m][0] = v[0]; st.w[m][1] = v[1]; st.w[m][2] = v[2]; st.w[m][3] = 0u;
-      }
-      if constexpr (SB == 1) {
-        if (a.scale_words) {
-          st.sc[m] = __builtin_amdgcn_raw_buffer_load_b32(R.rb[m], R.vb[m], bs1, 0);
-        } else {
-          uint32_t v = 0u;
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            v |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(R.rb[m], R.vb[m] + q, bs1, 0) << (8 * q);
-          st.sc[m] = v;
+      for (int h = 0; h < 2; ++h) {
+        if constexpr (BITS == 4) {
+          const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(R.rw[m], R.vw[m] + h * 4 * BLKB, ws, 0);
+          st.w[m][h][0] = v[0]; st.w[m][h][1] = v[1]; st.w[m][h][2] = v[2]; st.w[m][h][3] = v[3];
+        } else {
+          const auto v = __builtin_amdgcn_raw_buffer_load_b96(R.rw[m], R.vw[m] + h * 4 * BLKB, ws, 0);
+          st.w[m][h][0] = v[0]; st.w[m][h][1] = v[1]; st.w[m][h][2] = v[2]; st.w[m][h][3] = 0u;
         }
-      } else {
-        st.sc[m] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(R.rb[m], R.vb[m], bs4, 0);
       }
+      if constexpr (SB == 1) {            // the unit's 8 block scales
+        const int bs = real ? 8 * s : kOOR;
+        if (a.scale_words) {
+          const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(R.rb[m], R.vb[m], bs, 0);
+          st.sc[m][0] = v[0];
+          st.sc[m][1] = v[1];
+        } else {
+          uint32_t v0 = 0u, v1 = 0u;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            v0 |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(R.rb[m], R.vb[m] + q, bs, 0) << (8 * q);
+            v1 |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(R.rb[m], R.vb[m] + 4 + q, bs, 0) << (8 * q);
+          }
+          st.sc[m][0] = v0;
+          st.sc[m][1] = v1;
+        }
+      } else {                            // its 2 block scales
+        const int bs = real ? 2 * s : kOOR;
+        if (a.scale_words) {
+          st.sc[m][0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(R.rb[m], R.vb[m], bs, 0);
+        } else {
+          st.sc[m][0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(R.rb[m], R.vb[m], bs, 0) |
+                        ((uint32_t)__builtin_amdgcn_raw_buffer_load_b8(R.rb[m], R.vb[m] + 1, bs, 0) << 8);
+        }
+      }
+    }
+  };
+
+  // ---- activation stream: the tiles of the next trip, one dword per lane per (unit, step, subtile)
+  const int x_rows = (int)((a.num_slots + a.a_div - 1) / a.a_div);
+  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(a.x, (int64_t)x_rows * a.s_xm * 2);
+  // lane dword of a step's tile: wave w, lane l -> slot l / 4 of the subtile, inputs
+  // 32 (w / 4) + 8 (w % 4) + 2 (l % 4) of the step (the fragment layout the MFMA reads)
+  const int xcol = (wave >> 2) * 64 + (wave & 3) * 16 + (lane & 3) * 4;
+  int vx[MT];
+  int ax_b = -1;
+  auto act_rows = [&](int b) {
+    const int e = expert_of(b);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {            // padding slots fetch nothing
+      const int slot = slots[b * BM + mt * 16 + (lane >> 2)];
+      vx[mt] = (e >= 0 && slot < a.num_slots) ? (int)((int64_t)(slot / a.a_div) * a.s_xm * 2) + xcol : kOOR;
+    }
+  };
+  uint32_t ax[P][2][MT];
+  Pos ap{0, (int)(item0 - pm0 * nrt), (int)(ub - item0 * nun)};
+  int ja = 0;
+  auto act_trip = [&]() {                        // loads of the next P units' tiles
+#pragma unroll
+    for (int d = 0; d < P; ++d) {
+      const bool real = ja < n;
+      const int b = min(ap.pm, MAXBLK - 1);
+      if (real && b != ax_b) {
+        act_rows(b);
+        ax_b = b;
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int xs = real ? (2 * ap.s + h) * 256 : kOOR;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) ax[d][h][mt] = __builtin_amdgcn_raw_buffer_load_b32(rx, vx[mt], xs, 0);
+      }
+      advance(ap);
+      ++ja;
     }
   };
 
   // ---- compute stream
   f32x4 acc[MT][NM];
-  auto compute = [&](int s, const Stage<BITS, MT, NM>& st, const uint32_t* tile) {
-    uint32_t r[NM][4];
+  auto compute = [&](int s, const Stage<BITS, MT, NM, SB>& st, const uint32_t* tiles) {
 #pragma unroll
-    for (int m = 0; m < NM; ++m) {
-      if constexpr (BITS == 4) {
+    for (int h = 0; h < 2; ++h) {
+      uint32_t r[NM][4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) r[m][j] = st.w[m][j];
-      } else {   // the block's 96-bit stream as four 24-bit fields of 8 codes
-        r[m][0] = st.w[m][0];
-        r[m][1] = __builtin_amdgcn_alignbit(st.w[m][1], st.w[m][0], 24);
-        r[m][2] = __builtin_amdgcn_alignbit(st.w[m][2], st.w[m][1], 16);
-        r[m][3] = st.w[m][2] >> 8;
+      for (int m = 0; m < NM; ++m) {
+        if constexpr (BITS == 4) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) r[m][j] = st.w[m][h][j];
+        } else {   // the block's 96-bit stream as four 24-bit fields of 8 codes
+          r[m][0] = st.w[m][h][0];
+          r[m][1] = __builtin_amdgcn_alignbit(st.w[m][h][1], st.w[m][h][0], 24);
+          r[m][2] = __builtin_amdgcn_alignbit(st.w[m][h][2], st.w[m][h][1], 16);
+          r[m][3] = st.w[m][h][2] >> 8;
+        }
+        transpose_rows4(r[m]);     // r[m][q] = field lg of block 8 s + 4 h + q
       }
-      transpose_rows4(r[m]);     // r[m][q] = field lg of block 4 s + q
-    }
-    const int nq = KF ? 4 : min(4, nb32 - 4 * s);
-    float sf[NM][4];
-    if constexpr (SB == 1) {
+      const int nq = KF ? 4 : min(4, nb32 - 8 * s - 4 * h);
+      float sf[NM][4];
+      if constexpr (SB == 1) {
 #pragma unroll
-      for (int m = 0; m < NM; ++m) fp8x4(st.sc[m], sf[m]);
-    }
-    f32x4 part[MT][NM];
+        for (int m = 0; m < NM; ++m) fp8x4(st.sc[m][h], sf[m]);
+      }
+      f32x4 part[MT][NM];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int m = 0; m < NM; ++m) part[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int m = 0; m < NM; ++m) part[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      if (q < nq) {
-        u32x4 b[NM];
+      for (int q = 0; q < 4; ++q) {
+        if (q < nq) {
+          u32x4 bq[NM];
 #pragma unroll
-        for (int m = 0; m < NM; ++m) b[m] = lookup8<BITS>(r[m][q], cb[m], tab);
+          for (int m = 0; m < NM; ++m) bq[m] = lookup8<BITS>(r[m][q], cb[m], tab);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const u32x4 ax = *reinterpret_cast<const u32x4*>(tile + mt * 1024 + q * 256 + lane * 4);
+          for (int mt = 0; mt < MT; ++mt) {
+            const u32x4 av = *reinterpret_cast<const u32x4*>(tiles + h * TILE + mt * 1024 + q * 256 + lane * 4);
 #pragma unroll
-          for (int m = 0; m < NM; ++m) {
-            if constexpr (SB == 1) {
-              const f32x4 p = mfma16x16x32<ADT>(ax, b[m], f32x4{0.f, 0.f, 0.f, 0.f});
-              acc[mt][m] += p * sf[m][q];
-            } else {
-              part[mt][m] = mfma16x16x32<ADT>(ax, b[m], part[mt][m]);
+            for (int m = 0; m < NM; ++m) {
+              if constexpr (SB == 1) {
+                const f32x4 pr = mfma16x16x32<ADT>(av, bq[m], f32x4{0.f, 0.f, 0.f, 0.f});
+                acc[mt][m] += pr * sf[m][q];
+              } else {
+                part[mt][m] = mfma16x16x32<ADT>(av, bq[m], part[mt][m]);
+              }
             }
           }
         }
       }
-    }
-    if constexpr (SB == 4) {
+      if constexpr (SB == 4) {
 #pragma unroll
-      for (int m = 0; m < NM; ++m) {
-        const float f = fp8x1(st.sc[m]);
+        for (int m = 0; m < NM; ++m) {
+          const float f = fp8x1((st.sc[m][0] >> (8 * h)) & 0xFFu);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[mt][m] += part[mt][m] * f;
+          for (int mt = 0; mt < MT; ++mt) acc[mt][m] += part[mt][m] * f;
+        }
       }
     }
   };
@@ -366,7 +415,7 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
   auto epilogue = [&](const Pos& p, int b, bool full, bool first) {
     if (!full) {
       const int64_t it = (pm0 + p.pm) * nrt + p.pn;
-      const int g_lo = owner(it * nsteps, U, G), g_hi = owner(it * nsteps + nsteps - 1, U, G);
+      const int g_lo = owner(it * nun, U, G), g_hi = owner(it * nun + nun - 1, U, G);
       const int which = first ? 0 : 1;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
@@ -377,7 +426,7 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
                                                  0, kCohere);
       }
       __builtin_amdgcn_s_waitcnt(0);     // the partial is visible device-wide before the count
-      int* cnt = a.counters + it * kWaves + wave;
+      int32_t* cnt = a.counters + it * kWaves + wave;
       int old = 0;
       if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       old = __builtin_amdgcn_readlane(old, 0);
@@ -393,7 +442,7 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
           for (int gg = g_lo; gg <= g_hi; ++gg) {
             f32x4 v = acc[mt][m];
             if (gg != g) {
-              const int w = (U * gg / G) / nsteps == it ? 0 : 1;
+              const int w = (U * gg / G) / nun == it ? 0 : 1;
               v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, part_off(gg, w, mt, m), 0, kCohere));
             }
             t = gg == g_lo ? v : t + v;
@@ -414,8 +463,8 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
         if (slot >= a.num_slots) continue;
         if constexpr (GLU) {
           const float gt = acc[mt][0][r] * es0;
-          const float h = gt / (1.0f + expf(-gt)) * (acc[mt][1][r] * es1);
-          reinterpret_cast<uint16_t*>(a.out)[(int64_t)slot * a.s_om + nrow] = (uint16_t)to_bits<ADT>(h);
+          const float hv = gt / (1.0f + expf(-gt)) * (acc[mt][1][r] * es1);
+          reinterpret_cast<uint16_t*>(a.out)[(int64_t)slot * a.s_om + nrow] = (uint16_t)to_bits<ADT>(hv);
         } else {
           const float y = acc[mt][0][r] * es0 * slot_w[row];
           reinterpret_cast<float*>(a.out)[(int64_t)slot * a.s_om + nrow] = y;
@@ -423,10 +472,10 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
       }
   };
 
-  // ---- prologue: descriptors and the first P steps in flight, then the rest of the staging
-  Pos cp{0, (int)(item0 - pm0 * nrt), (int)(ub - item0 * nsteps)};
+  // ---- prologue: descriptors and the first trip's loads in flight, then the rest of the staging
+  Pos cp{0, (int)(item0 - pm0 * nrt), (int)(ub - item0 * nun)};
   Pos lp = cp;
-  Stage<BITS, MT, NM> st[P];
+  Stage<BITS, MT, NM, SB> st[P];
   int jl = 0;
   setup(lp);
 #pragma unroll
@@ -436,8 +485,10 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
     advance(lp);
     ++jl;
   }
+  act_trip();
   for (int b = tid; b < MAXBLK; b += kThreads) {
     const int e = expert_of(b);
+    blk_e[b] = e;
 #pragma unroll
     for (int m = 0; m < NM; ++m) blk_es[b][m] = e >= 0 ? (m == 0 ? a.w0 : a.w1).expert_scale[e] : 0.f;
   }
@@ -448,26 +499,35 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
     const int e = expert_of(b);
     blk_lv[b][m][c] = e >= 0 ? (uint16_t)to_bits<ADT>((m == 0 ? a.w0 : a.w1).levels[(int64_t)e * L + c]) : 0;
   }
-  // (the first step's ring write below is followed by a barrier that also publishes these)
+  // (the first trip's barrier below also publishes these)
 
-  // ---- main loop over the range's units, P per trip so the register stages stay static
-  int cur_e = -1, sa = 0;
+  // ---- main loop: one trip of P units per iteration, one barrier per trip
+  int cur_e = -1, cur_b = -1, e = -1, sa = 0;
   bool first = true;
   for (int j0 = 0; j0 < n; j0 += P) {
+    uint32_t* tiles = ring[(j0 / P) & 1];
+#pragma unroll
+    for (int d = 0; d < P; ++d)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) tiles[(d * 2 + h) * TILE + mt * 1024 + wave * 64 + lane] = ax[d][h][mt];
+    act_trip();
+    __syncthreads();                   // the trip's tiles are complete; the previous trip's readers are done
 #pragma unroll
     for (int d = 0; d < P; ++d) {
       const int j = j0 + d;
       if (j < n) {
-        uint32_t* tile = ring[j & 1];
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) tile[mt * 1024 + wave * 64 + lane] = st[d].ax[mt];
-        __syncthreads();                 // the tile is complete; step j - 2's readers of this stage are done
         const int b = min(cp.pm, MAXBLK - 1);
-        const int e = __builtin_amdgcn_readfirstlane(expert_of(b));
-        if (e >= 0 && e != cur_e) {
-          build_table(b);
-          __syncthreads();
-          cur_e = e;
+        if (b != cur_b) {                // a new block: its expert and pair tables
+          cur_b = b;
+          e = __builtin_amdgcn_readfirstlane(blk_e[b]);
+          if (e >= 0 && e != cur_e) {
+            if (cur_e >= 0) __syncthreads();   // the old tables' readers are done
+            build_table(b);
+            __syncthreads();
+            cur_e = e;
+          }
         }
         if (j == 0 || cp.s == 0) {
           sa = cp.s;
@@ -478,8 +538,8 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
             for (int m = 0; m < NM; ++m) acc[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
         if (e >= 0) {
-          compute(cp.s, st[d], tile);
-          if (cp.s == nsteps - 1 || j == n - 1) epilogue(cp, b, sa == 0 && cp.s == nsteps - 1, first);
+          compute(cp.s, st[d], tiles + d * 2 * TILE);
+          if (cp.s == nun - 1 || j == n - 1) epilogue(cp, b, sa == 0 && cp.s == nun - 1, first);
         }
         advance(cp);
       }
@@ -523,13 +583,14 @@ __global__ __launch_bounds__(256) void moe_reduce_kernel(const float* __restrict
 
 template <int BITS, int ADT, bool GLU, int MT>
 static void launch_sb(int sb, dim3 grid, hipStream_t st, const MoeArgs& a) {
-  const bool kf = (a.K / kHexBlock) % 4 == 0;     // whole 128-input steps: no tail checks
+  const bool kf = (a.K / kHexBlock) % 8 == 0;     // whole 256-input units: no tail checks
   const dim3 block(kThreads);
   if (sb == 1) {
     if (kf) hipLaunchKernelGGL((hex_moe_kernel<BITS, ADT, GLU, MT, 1, true>), grid, block, 0, st, a);
     else hipLaunchKernelGGL((hex_moe_kernel<BITS, ADT, GLU, MT, 1, false>), grid, block, 0, st, a);
-  } else {   // 128-input scale blocks imply whole steps
-    hipLaunchKernelGGL((hex_moe_kernel<BITS, ADT, GLU, MT, 4, true>), grid, block, 0, st, a);
+  } else {
+    if (kf) hipLaunchKernelGGL((hex_moe_kernel<BITS, ADT, GLU, MT, 4, true>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((hex_moe_kernel<BITS, ADT, GLU, MT, 4, false>), grid, block, 0, st, a);
   }
 }
 
@@ -566,10 +627,10 @@ static int device_cus() {
 }
 
 // Persistent grid: one workgroup per compute unit, fewer when the plan's units (an upper bound
-// from num_blocks) would give a workgroup fewer than kMinUnits steps, and enough that no
+// from num_blocks) would give a workgroup fewer than kMinUnits units, and enough that no
 // workgroup's range spans more expert blocks than it stages in LDS (64 / MT).
 static int64_t moe_grid(int64_t num_blocks, int64_t n_out, int64_t n_in, int mt) {
-  const int64_t units = num_blocks * cdiv(n_out, kRows) * cdiv(cdiv(n_in, kHexBlock), 4);
+  const int64_t units = num_blocks * cdiv(n_out, kRows) * cdiv(cdiv(n_in, kHexBlock), 8);
   int64_t g = cdiv(units, kMinUnits);
   if (g > device_cus()) g = device_cus();
   const int64_t min_g = cdiv(num_blocks, kMaxBlk16 / mt - 2);
@@ -577,15 +638,16 @@ static int64_t moe_grid(int64_t num_blocks, int64_t n_out, int64_t n_in, int mt)
   return g > 0 ? g : 1;
 }
 
+// Workspace of one launch: arrival counters (one per item and wave) and partial-sum tiles (two
+// per workgroup and wave), as two separate buffers so calls of any shape can share them.
 struct Workspace {
-  int64_t counter_bytes, part_bytes;
+  int64_t counters, partials;      // int32 counters, float partials
 };
 
 static Workspace workspace_layout(int64_t num_blocks, int64_t n_out, int64_t n_in, int mt, bool glu) {
-  const int64_t items = num_blocks * cdiv(n_out, kRows);
   Workspace w;
-  w.counter_bytes = cdiv(items * kWaves * 4, 256) * 256;
-  w.part_bytes = moe_grid(num_blocks, n_out, n_in, mt) * 2 * kWaves * (int64_t)mt * (glu ? 2 : 1) * kWave * 16;
+  w.counters = num_blocks * cdiv(n_out, kRows) * kWaves;
+  w.partials = moe_grid(num_blocks, n_out, n_in, mt) * 2 * kWaves * (int64_t)mt * (glu ? 2 : 1) * kWave * 4;
   return w;
 }
 
@@ -621,16 +683,17 @@ static int check_moe(const char* who, int32_t bits, int32_t adt, int64_t n_out, 
   return BH_HEX_OK;
 }
 
-// Points the kernel at the caller's workspace: counters first, then the partial sums.
-static int attach_workspace(const char* who, void* ws, int64_t ws_bytes, int64_t num_blocks, int64_t n_out,
-                            int64_t n_in, int mt, bool glu, MoeArgs& a, dim3* grid) {
+// Points the kernel at the caller's workspace.
+static int attach_workspace(const char* who, int32_t* counters, int64_t n_counters, float* partials,
+                            int64_t n_partials, int64_t num_blocks, int64_t n_out, int64_t n_in, int mt, bool glu,
+                            MoeArgs& a, dim3* grid) {
   const Workspace w = workspace_layout(num_blocks, n_out, n_in, mt, glu);
-  if (!ws || ws_bytes < w.counter_bytes + w.part_bytes)
-    return fail(BH_HEX_ERR_VALUE, std::string(who) + ": workspace smaller than bh_hex_moe_workspace_bytes()");
-  if (!aligned(ws, 256)) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": workspace must be 256-byte aligned");
-  if (w.part_bytes > 0x7FFFFFFF) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": plan too large");
-  a.counters = reinterpret_cast<int*>(ws);
-  a.part = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + w.counter_bytes);
+  if (!counters || !partials || n_counters < w.counters || n_partials < w.partials)
+    return fail(BH_HEX_ERR_VALUE, std::string(who) + ": workspace smaller than bh_hex_moe_workspace() asks");
+  if (!aligned(partials, 16)) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": partials must be 16-byte aligned");
+  if (w.partials * 4 > 0x7FFFFFFF) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": plan too large");
+  a.counters = counters;
+  a.part = partials;
   *grid = dim3((unsigned)moe_grid(num_blocks, n_out, n_in, mt));
   return BH_HEX_OK;
 }
@@ -644,8 +707,9 @@ static int proj_setup(const char* who, const bh_hex_proj* w, int bits, int64_t n
   *sb = block / 32;
   if (bits == 4 && (w->s_ie % 4 || w->s_in % 4 || !aligned(w->idx, 16)))
     return fail(BH_HEX_ERR_VALUE, std::string(who) + ": 4-bit idx rows must be 16-byte aligned");
-  const int64_t nb32 = n_in / kHexBlock;
-  if (nb32 % 4 || w->s_bn % 4 || w->s_be % 4 || !aligned(w->block_scale, 4)) *words = 0;
+  // a unit's scales in one load: 8 bytes at 32-input blocks, 2 bytes at 128-input blocks
+  const int sw = block == 32 ? 8 : 2;
+  if (w->s_bn % sw || w->s_be % sw || !aligned(w->block_scale, sw)) *words = 0;
   return BH_HEX_OK;
 }
 
@@ -657,8 +721,8 @@ extern "C" int bh_hex_moe_glu(const void* x, int32_t x_dtype, int64_t s_xm, void
                               const bh_hex_proj* gate, const bh_hex_proj* up, int32_t bits, int64_t n_out, int64_t n_in,
                               const int32_t* sorted_ids, const int32_t* expert_ids, int64_t num_blocks,
                               const int32_t* npp, const int32_t* lookup, int32_t n_experts, int64_t num_slots,
-                              int32_t a_div, const bh_hex_tile* tile, void* workspace, int64_t workspace_bytes,
-                              void* stream) {
+                              int32_t a_div, const bh_hex_tile* tile, int32_t* counters, int64_t n_counters,
+                              float* partials, int64_t n_partials, void* stream) {
   const char* who = "bh_hex_moe_glu";
   MoeArgs a{};
   int mt = 0, sb = 0, words = 1;
@@ -673,7 +737,8 @@ extern "C" int bh_hex_moe_glu(const void* x, int32_t x_dtype, int64_t s_xm, void
   if (cdiv(num_slots, a_div) * s_xm * 2 > 0x7FFFFFFF) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": x over 2 GiB");
   if (num_blocks == 0 || num_slots == 0) return BH_HEX_OK;
   dim3 grid;
-  if ((rc = attach_workspace(who, workspace, workspace_bytes, num_blocks, n_out, n_in, mt, true, a, &grid))) return rc;
+  if ((rc = attach_workspace(who, counters, n_counters, partials, n_partials, num_blocks, n_out, n_in, mt, true, a,
+                             &grid))) return rc;
   a.x = reinterpret_cast<const uint16_t*>(x);
   a.s_xm = s_xm;
   a.out = act;
@@ -690,8 +755,8 @@ extern "C" int bh_hex_moe_down(const void* act, int32_t act_dtype, int64_t s_am,
                                const bh_hex_proj* down, int32_t bits, int64_t n_out, int64_t n_in,
                                const int32_t* sorted_ids, const int32_t* expert_ids, int64_t num_blocks,
                                const int32_t* npp, const int32_t* lookup, int32_t n_experts, int64_t num_slots,
-                               const float* topk_w, const bh_hex_tile* tile, void* workspace, int64_t workspace_bytes,
-                               void* stream) {
+                               const float* topk_w, const bh_hex_tile* tile, int32_t* counters, int64_t n_counters,
+                               float* partials, int64_t n_partials, void* stream) {
   const char* who = "bh_hex_moe_down";
   MoeArgs a{};
   int mt = 0, sb = 0, words = 1;
@@ -704,7 +769,8 @@ extern "C" int bh_hex_moe_down(const void* act, int32_t act_dtype, int64_t s_am,
   if (num_slots * s_am * 2 > 0x7FFFFFFF) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": act over 2 GiB");
   if (num_blocks == 0 || num_slots == 0) return BH_HEX_OK;
   dim3 grid;
-  if ((rc = attach_workspace(who, workspace, workspace_bytes, num_blocks, n_out, n_in, mt, false, a, &grid))) return rc;
+  if ((rc = attach_workspace(who, counters, n_counters, partials, n_partials, num_blocks, n_out, n_in, mt, false, a,
+                             &grid))) return rc;
   a.x = reinterpret_cast<const uint16_t*>(act);
   a.s_xm = s_am;
   a.out = y;
@@ -718,11 +784,16 @@ extern "C" int bh_hex_moe_down(const void* act, int32_t act_dtype, int64_t s_am,
   return check_launch(who);
 }
 
-extern "C" int64_t bh_hex_moe_workspace_bytes(int64_t num_blocks, int64_t n_out, int64_t n_in, int32_t block_m,
-                                              int32_t glu) {
-  if (num_blocks < 0 || n_out <= 0 || n_in <= 0 || (block_m != 16 && block_m != 32 && block_m != 64)) return -1;
+extern "C" int bh_hex_moe_workspace(int64_t num_blocks, int64_t n_out, int64_t n_in, int32_t block_m, int32_t glu,
+                                    int64_t* n_counters, int64_t* n_partials) {
+  if (num_blocks < 0 || n_out <= 0 || n_in <= 0 || !n_counters || !n_partials)
+    return fail(BH_HEX_ERR_VALUE, "bh_hex_moe_workspace: bad arguments");
+  if (block_m != 16 && block_m != 32 && block_m != 64)
+    return fail(BH_HEX_ERR_UNSUPPORTED, "bh_hex_moe_workspace: block_m must be 16, 32 or 64");
   const Workspace w = workspace_layout(num_blocks, n_out, n_in, block_m / 16, glu != 0);
-  return w.counter_bytes + w.part_bytes;
+  *n_counters = w.counters;
+  *n_partials = w.partials;
+  return BH_HEX_OK;
 }
 
 extern "C" int bh_hex_moe_reduce(const float* y, int64_t s_ym, const void* topk_ids, int32_t ids_dtype,

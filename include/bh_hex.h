@@ -123,7 +123,8 @@ int bh_hex_moe_glu(const void* x, int32_t x_dtype, int64_t s_xm, void* act, int6
                    const bh_hex_proj* gate, const bh_hex_proj* up, int32_t bits, int64_t n_out, int64_t n_in,
                    const int32_t* sorted_ids, const int32_t* expert_ids, int64_t num_blocks, const int32_t* npp,
                    const int32_t* lookup, int32_t n_experts, int64_t num_slots, int32_t a_div,
-                   const bh_hex_tile* tile, void* workspace, int64_t workspace_bytes, void* stream);
+                   const bh_hex_tile* tile, int32_t* counters, int64_t n_counters, float* partials,
+                   int64_t n_partials, void* stream);
 
 /* The down half over one tier: y[s, o] = (es_d * sum_i act[s, i] W_d[o, i]) * topk_w[s],
  * written as float32 y [num_slots, n_out] (row stride s_ym) for the slots of every block of
@@ -132,16 +133,20 @@ int bh_hex_moe_down(const void* act, int32_t act_dtype, int64_t s_am, float* y, 
                     const bh_hex_proj* down, int32_t bits, int64_t n_out, int64_t n_in,
                     const int32_t* sorted_ids, const int32_t* expert_ids, int64_t num_blocks, const int32_t* npp,
                     const int32_t* lookup, int32_t n_experts, int64_t num_slots, const float* topk_w,
-                    const bh_hex_tile* tile, void* workspace, int64_t workspace_bytes, void* stream);
+                    const bh_hex_tile* tile, int32_t* counters, int64_t n_counters, float* partials,
+                   int64_t n_partials, void* stream);
 
-/* Device workspace bytes bh_hex_moe_glu (glu != 0) or bh_hex_moe_down needs for a plan of
- * num_blocks blocks of block_m slots over n_out x n_in projections, on the current device
- * (-1 for bad arguments). The workspace (256-byte aligned) must be zero-filled before its first
- * use; every call leaves it zero-filled again, so it can be kept and reused. Calls that share a
- * workspace must not overlap in time (one stream, or ordered streams). No counterpart in the
- * reference, whose Triton kernels need none: it holds per-item arrival counters and the partial
- * sums of items whose inputs are split between workgroups. */
-int64_t bh_hex_moe_workspace_bytes(int64_t num_blocks, int64_t n_out, int64_t n_in, int32_t block_m, int32_t glu);
+/* Device workspace that bh_hex_moe_glu (glu != 0) or bh_hex_moe_down needs for a plan of
+ * num_blocks blocks of block_m slots over n_out x n_in projections on the current device:
+ * *n_counters int32 arrival counters and *n_partials floats (16-byte aligned) of partial sums.
+ * The counters must be zero before their first use; every call leaves them zero again, so one
+ * workspace, sized for the largest call, can be kept and shared by calls of any shape. The
+ * partials need no initial value. Calls that share a workspace must not overlap in time (one
+ * stream, or ordered streams). No counterpart in the reference, whose Triton kernels need none:
+ * the kernels split an item's inputs between workgroups, and the last workgroup to arrive adds
+ * the others' partial sums. */
+int bh_hex_moe_workspace(int64_t num_blocks, int64_t n_out, int64_t n_in, int32_t block_m, int32_t glu,
+                         int64_t* n_counters, int64_t* n_partials);
 
 /* out[t, h] = sum_j y[t * k + j, h] over the token's k slots, in float32, rounded once to
  * out_dtype (F32, BF16 or F16); slots whose id (topk_ids, I32 or I64) is outside

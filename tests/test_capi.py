@@ -44,15 +44,20 @@ def test_align_max_blocks_formula():
     assert lib.bh_hex_align_max_blocks(4, 4, 0) == -1
 
 
-def test_workspace_bytes():
+def _workspace(lib, *args):
+    nc, npart = ctypes.c_int64(), ctypes.c_int64()
+    rc = lib.bh_hex_moe_workspace(*args, ctypes.byref(nc), ctypes.byref(npart))
+    return rc, nc.value, npart.value
+
+
+def test_workspace_sizes():
     lib = _lib.load()
-    assert lib.bh_hex_moe_workspace_bytes(-1, 64, 64, 16, 1) == -1
-    assert lib.bh_hex_moe_workspace_bytes(4, 64, 64, 24, 1) == -1
-    glu = lib.bh_hex_moe_workspace_bytes(104, 768, 2048, 16, 1)
-    down = lib.bh_hex_moe_workspace_bytes(104, 2048, 768, 16, 0)
-    assert glu > 0 and down > 0 and glu % 256 == 0 and down % 256 == 0
-    # counters (items x 16 waves) plus partial tiles, which grow with block_m
-    assert lib.bh_hex_moe_workspace_bytes(104, 768, 2048, 64, 1) > glu
+    assert _workspace(lib, -1, 64, 64, 16, 1)[0] == _lib.ERR_VALUE
+    assert _workspace(lib, 4, 64, 64, 24, 1)[0] == _lib.ERR_UNSUPPORTED
+    rc, nc, npart = _workspace(lib, 104, 768, 2048, 16, 1)
+    assert rc == _lib.OK and nc == 104 * 3 * 16 and npart > 0
+    rc, nc2, npart2 = _workspace(lib, 104, 768, 2048, 64, 1)
+    assert nc2 == nc and npart2 > npart          # partial tiles grow with block_m
 
 
 def _status(rc, code, pattern):
@@ -80,16 +85,16 @@ def test_host_side_errors():
             _lib.ERR_VALUE, "scale block")
     for bad in (_lib.HexTile(16, 32, 1), _lib.HexTile(32, 256, 2)):
         _status(lib.bh_hex_moe_glu(16, _lib.BF16, 64, 16, 64, ctypes.byref(w), ctypes.byref(w), 4, 64, 64,
-                                   16, 16, 1, 16, 16, 4, 4, 1, ctypes.byref(bad), None, 0, None),
+                                   16, 16, 1, 16, 16, 4, 4, 1, ctypes.byref(bad), None, 0, None, 0, None),
                 _lib.ERR_UNSUPPORTED, "block_n must be 256")
     tile = _lib.HexTile(16, 256, 1)
     _status(lib.bh_hex_moe_glu(16, _lib.F32, 64, 16, 64, ctypes.byref(w), ctypes.byref(w), 4, 64, 64,
-                               16, 16, 1, 16, 16, 4, 4, 1, ctypes.byref(tile), None, 0, None),
+                               16, 16, 1, 16, 16, 4, 4, 1, ctypes.byref(tile), None, 0, None, 0, None),
             _lib.ERR_UNSUPPORTED, "BF16 or F16")
     # a plan with blocks needs the workspace (checked before anything reaches the device)
     w32 = _lib.HexProj(16, 16, 16, 16, 0, 4, 0, 1, 32)
     _status(lib.bh_hex_moe_glu(16, _lib.BF16, 64, 16, 64, ctypes.byref(w32), ctypes.byref(w32), 4, 64, 64,
-                               16, 16, 1, 16, 16, 4, 4, 1, ctypes.byref(tile), None, 0, None),
+                               16, 16, 1, 16, 16, 4, 4, 1, ctypes.byref(tile), None, 0, None, 0, None),
             _lib.ERR_VALUE, "workspace")
     _status(lib.bh_hex_moe_reduce(16, 6, 16, _lib.I64, 4, 2, 2, 6, 16, _lib.BF16, 6, None),
             _lib.ERR_UNSUPPORTED, "H % 4")
