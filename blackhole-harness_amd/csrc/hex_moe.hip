@@ -31,6 +31,7 @@
 // Weights therefore enter the matrix cores as round(level) and the block scale is applied to
 // the float32 block partial, where the reference rounds level * fp8 to the activation dtype.
 #include <string>
+#include <type_traits>
 
 #include "hex_common.h"
 
@@ -54,6 +55,7 @@ struct MoeArgs {
   int32_t a_div;
   int32_t N, K;
   int32_t scale_words;   // block_scale rows allow one load of a unit's scales (8 or 2 bytes)
+                         // (host only: it selects the whole-unit kernel variant)
   float* part;           // workspace: partial sums of items split between workgroups
   int32_t* counters;     // workspace: arrivals per (item, wave), zero between calls
 };
@@ -94,22 +96,71 @@ __device__ __forceinline__ u32x4 lookup8(uint32_t f, uint32_t cb, const uint32_t
 }
 
 // One unit's loads of one wave: two 128-input steps.
-template <int BITS, int MT, int NM, int SB>
+template <int BITS, int NM, int SB, bool KF>
 struct Stage {
-  uint32_t w[NM][2][4];  // per step, the lane's 32-input block (4-bit: 4 words; 3-bit: 3)
-  uint32_t sc[NM][SB == 1 ? 2 : 1];   // fp8 block scales of the row: 8 bytes (B = 32) or 2 (B = 128)
+  using W = typename std::conditional<BITS == 4, u32x4, u32x3>::type;
+  W w[NM][2];            // per step, the lane's 32-input block (4-bit: 4 words; 3-bit: 3)
+  // fp8 block scales of the row: whole units read them in one load (8 bytes at B = 32, 2 at
+  // B = 128); the tail variant reads them byte by byte
+  typename std::conditional<SB == 1, u32x2, uint32_t>::type scw[NM];
+  uint32_t scb[NM][KF ? 1 : (SB == 1 ? 8 : 2)];
 };
 
-// Buffer resources and per-lane byte offsets of the weight stream's current item. Each
-// resource spans one expert's matrix, so loads past its end return zero instead of faulting;
-// rows past the matrix read out of range (nothing fetched) and are never stored. The unit
-// offset goes in the scalar soffset, so a unit costs no vector address math.
+// Buffer descriptors of the weight stream's current item, as four SGPRs each (the hot loop's
+// loads are hand-scheduled, below). Each spans one expert's matrix, so loads past its end return
+// zero instead of faulting; rows past the matrix read out of range (nothing fetched) and are
+// never stored. The unit offset goes in the scalar soffset.
 template <int NM>
 struct ItemRes {
-  __amdgpu_buffer_rsrc_t rw[NM];   // packed index words of the item's expert
-  __amdgpu_buffer_rsrc_t rb[NM];   // its fp8 block scales
-  int vw[NM], vb[NM];              // lane offsets: row n, block lane / 16 of the unit
+  u32x4 rw[NM];          // packed index words of the item's expert
+  u32x4 rb[NM];          // its fp8 block scales
+  int vw[NM], vb[NM];    // lane offsets: row n, block lane / 16 of the unit
 };
+
+// Hand-scheduled buffer loads. The compiler does not see these as memory operations, so it
+// inserts no waits for them; the kernel waits with explicit s_waitcnt vmcnt(N) whose operands
+// are the loaded registers (so no use can move above the wait). N counts the loads issued after
+// the awaited ones in program order; any other memory operation issued in between only makes
+// the wait stricter, so conditional stores cannot break it.
+__device__ __forceinline__ u32x4 make_desc(const void* base, int64_t bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  const uint32_t n = (uint32_t)(bytes > 0x7FFFFFFF ? 0x7FFFFFFF : bytes);
+  return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)p),
+               (uint32_t)__builtin_amdgcn_readfirstlane((int)((uint32_t)(p >> 32) & 0xFFFFu)),
+               (uint32_t)__builtin_amdgcn_readfirstlane((int)n), 0x00020000u};
+}
+template <int IMM>
+__device__ __forceinline__ void ld_x4(u32x4& d, const u32x4& r, int v, int s) {
+  asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen offset:%4" : "=v"(d) : "v"(v), "s"(r), "s"(s), "i"(IMM));
+}
+template <int IMM>
+__device__ __forceinline__ void ld_x3(u32x3& d, const u32x4& r, int v, int s) {
+  asm volatile("buffer_load_dwordx3 %0, %1, %2, %3 offen offset:%4" : "=v"(d) : "v"(v), "s"(r), "s"(s), "i"(IMM));
+}
+template <int IMM>
+__device__ __forceinline__ void ld_x2(u32x2& d, const u32x4& r, int v, int s) {
+  asm volatile("buffer_load_dwordx2 %0, %1, %2, %3 offen offset:%4" : "=v"(d) : "v"(v), "s"(r), "s"(s), "i"(IMM));
+}
+template <int IMM>
+__device__ __forceinline__ void ld_x1(uint32_t& d, const u32x4& r, int v, int s) {
+  asm volatile("buffer_load_dword %0, %1, %2, %3 offen offset:%4" : "=v"(d) : "v"(v), "s"(r), "s"(s), "i"(IMM));
+}
+template <int IMM>
+__device__ __forceinline__ void ld_u16(uint32_t& d, const u32x4& r, int v, int s) {
+  asm volatile("buffer_load_ushort %0, %1, %2, %3 offen offset:%4" : "=v"(d) : "v"(v), "s"(r), "s"(s), "i"(IMM));
+}
+template <int IMM>
+__device__ __forceinline__ void ld_u8(uint32_t& d, const u32x4& r, int v, int s) {
+  asm volatile("buffer_load_ubyte %0, %1, %2, %3 offen offset:%4" : "=v"(d) : "v"(v), "s"(r), "s"(s), "i"(IMM));
+}
+template <int N, typename T>
+__device__ __forceinline__ void vm_wait(T& x) {      // wait until at most N loads are outstanding
+  asm volatile("s_waitcnt vmcnt(%1)" : "+v"(x) : "i"(N));
+}
+template <typename T>
+__device__ __forceinline__ void after_wait(T& x) {   // order x's uses after the wait just above
+  asm volatile("" : "+v"(x));
+}
 
 constexpr int kRsrcWord3 = 0x00020000;   // raw buffer, 32-bit data format (gfx9 family)
 constexpr int kCohere = 16;              // cache policy sc1: coherent across the device's L2s
@@ -236,59 +287,69 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
       const bh_hex_proj& w = m == 0 ? a.w0 : a.w1;
-      R.rw[m] = buffer_rsrc(w.idx + ee * w.s_ie, (int64_t)a.N * w.s_in * 4);
-      R.rb[m] = buffer_rsrc(w.block_scale + ee * w.s_be, (int64_t)a.N * w.s_bn);
+      R.rw[m] = make_desc(w.idx + ee * w.s_ie, (int64_t)a.N * w.s_in * 4);
+      R.rb[m] = make_desc(w.block_scale + ee * w.s_be, (int64_t)a.N * w.s_bn);
       R.vw[m] = rv ? (int)(nrow * w.s_in * 4) + lg * BLKB : kOOR;
       R.vb[m] = rv ? (int)(nrow * w.s_bn) : kOOR;
     }
   };
-  // loads of unit s of the current descriptors; dummy units (past the range) read out of range
-  auto load = [&](int s_, bool real, Stage<BITS, MT, NM, SB>& st) {
+  // loads of unit s of the current descriptors; dummy units (past the range) read out of range.
+  // WU loads per unit, in this order: per matrix the two steps' blocks, then its scales.
+  constexpr int SCN = KF ? 1 : (SB == 1 ? 8 : 2);
+  constexpr int WU = NM * (2 + SCN);
+  // The whole byte offset goes in the range-checked VGPR offset (soffset 0): dummy units and
+  // invalid rows sit past every resource.
+  auto load = [&](int s_, bool real, Stage<BITS, NM, SB, KF>& st) {
     const int s = __builtin_amdgcn_readfirstlane(real ? s_ : 0);
     const int ws = real ? s * USTEP : kOOR;
+    const int bs = real ? (SB == 1 ? 8 : 2) * s : kOOR;
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        if constexpr (BITS == 4) {
-          const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(R.rw[m], R.vw[m] + h * 4 * BLKB, ws, 0);
-          st.w[m][h][0] = v[0]; st.w[m][h][1] = v[1]; st.w[m][h][2] = v[2]; st.w[m][h][3] = v[3];
-        } else {
-          const auto v = __builtin_amdgcn_raw_buffer_load_b96(R.rw[m], R.vw[m] + h * 4 * BLKB, ws, 0);
-          st.w[m][h][0] = v[0]; st.w[m][h][1] = v[1]; st.w[m][h][2] = v[2]; st.w[m][h][3] = 0u;
+      const int vw = R.vw[m] + ws, vb = R.vb[m] + bs;
+      if constexpr (BITS == 4) {
+        ld_x4<0>(st.w[m][0], R.rw[m], vw, 0);
+        ld_x4<4 * BLKB>(st.w[m][1], R.rw[m], vw, 0);
+      } else {
+        ld_x3<0>(st.w[m][0], R.rw[m], vw, 0);
+        ld_x3<4 * BLKB>(st.w[m][1], R.rw[m], vw, 0);
+      }
+      if constexpr (KF) {
+        if constexpr (SB == 1) ld_x2<0>(st.scw[m], R.rb[m], vb, 0);
+        else ld_u16<0>(st.scw[m], R.rb[m], vb, 0);
+      } else {
+        ld_u8<0>(st.scb[m][0], R.rb[m], vb, 0);
+        ld_u8<1>(st.scb[m][1], R.rb[m], vb, 0);
+        if constexpr (SB == 1) {
+          ld_u8<2>(st.scb[m][2], R.rb[m], vb, 0);
+          ld_u8<3>(st.scb[m][3], R.rb[m], vb, 0);
+          ld_u8<4>(st.scb[m][4], R.rb[m], vb, 0);
+          ld_u8<5>(st.scb[m][5], R.rb[m], vb, 0);
+          ld_u8<6>(st.scb[m][6], R.rb[m], vb, 0);
+          ld_u8<7>(st.scb[m][7], R.rb[m], vb, 0);
         }
       }
-      if constexpr (SB == 1) {            // the unit's 8 block scales
-        const int bs = real ? 8 * s : kOOR;
-        if (a.scale_words) {
-          const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(R.rb[m], R.vb[m], bs, 0);
-          st.sc[m][0] = v[0];
-          st.sc[m][1] = v[1];
-        } else {
-          uint32_t v0 = 0u, v1 = 0u;
+    }
+  };
+  // wait for a stage's loads, with N later loads allowed in flight
+  auto wait_stage = [&](auto n_later, Stage<BITS, NM, SB, KF>& st) {
+    constexpr int N = decltype(n_later)::value;
+    vm_wait<N>(st.w[0][0]);
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            v0 |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(R.rb[m], R.vb[m] + q, bs, 0) << (8 * q);
-            v1 |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(R.rb[m], R.vb[m] + 4 + q, bs, 0) << (8 * q);
-          }
-          st.sc[m][0] = v0;
-          st.sc[m][1] = v1;
-        }
-      } else {                            // its 2 block scales
-        const int bs = real ? 2 * s : kOOR;
-        if (a.scale_words) {
-          st.sc[m][0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(R.rb[m], R.vb[m], bs, 0);
-        } else {
-          st.sc[m][0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(R.rb[m], R.vb[m], bs, 0) |
-                        ((uint32_t)__builtin_amdgcn_raw_buffer_load_b8(R.rb[m], R.vb[m] + 1, bs, 0) << 8);
-        }
+    for (int m = 0; m < NM; ++m) {
+      if (m > 0) after_wait(st.w[m][0]);
+      after_wait(st.w[m][1]);
+      if constexpr (KF) {
+        after_wait(st.scw[m]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < SCN; ++i) after_wait(st.scb[m][i]);
       }
     }
   };
 
   // ---- activation stream: the tiles of the next trip, one dword per lane per (unit, step, subtile)
   const int x_rows = (int)((a.num_slots + a.a_div - 1) / a.a_div);
-  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(a.x, (int64_t)x_rows * a.s_xm * 2);
+  const u32x4 rx = make_desc(a.x, (int64_t)x_rows * a.s_xm * 2);
   // lane dword of a step's tile: wave w, lane l -> slot l / 4 of the subtile, inputs
   // 32 (w / 4) + 8 (w % 4) + 2 (l % 4) of the step (the fragment layout the MFMA reads)
   const int xcol = (wave >> 2) * 64 + (wave & 3) * 16 + (lane & 3) * 4;
@@ -302,10 +363,12 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
       vx[mt] = (e >= 0 && slot < a.num_slots) ? (int)((int64_t)(slot / a.a_div) * a.s_xm * 2) + xcol : kOOR;
     }
   };
+  constexpr int AT = P * 2 * MT;                 // activation loads per trip
   uint32_t ax[P][2][MT];
   Pos ap{0, (int)(item0 - pm0 * nrt), (int)(ub - item0 * nun)};
   int ja = 0;
   auto act_trip = [&]() {                        // loads of the next P units' tiles
+    int xs[P][2], vxd[P][MT];
 #pragma unroll
     for (int d = 0; d < P; ++d) {
       const bool real = ja < n;
@@ -315,19 +378,23 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
         ax_b = b;
       }
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int xs = real ? (2 * ap.s + h) * 256 : kOOR;
+      for (int mt = 0; mt < MT; ++mt) vxd[d][mt] = vx[mt];
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) ax[d][h][mt] = __builtin_amdgcn_raw_buffer_load_b32(rx, vx[mt], xs, 0);
-      }
+      for (int h = 0; h < 2; ++h) xs[d][h] = __builtin_amdgcn_readfirstlane(real ? (2 * ap.s + h) * 256 : kOOR);
       advance(ap);
       ++ja;
     }
+#pragma unroll
+    for (int d = 0; d < P; ++d)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) ld_x1<0>(ax[d][h][mt], rx, vxd[d][mt] + xs[d][h], 0);
   };
 
   // ---- compute stream
   f32x4 acc[MT][NM];
-  auto compute = [&](int s, const Stage<BITS, MT, NM, SB>& st, const uint32_t* tiles) {
+  auto compute = [&](int s, const Stage<BITS, NM, SB, KF>& st, const uint32_t* tiles) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       uint32_t r[NM][4];
@@ -348,7 +415,12 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
       float sf[NM][4];
       if constexpr (SB == 1) {
 #pragma unroll
-        for (int m = 0; m < NM; ++m) fp8x4(st.sc[m][h], sf[m]);
+        for (int m = 0; m < NM; ++m) {
+          uint32_t w4;
+          if constexpr (KF) w4 = st.scw[m][h];
+          else w4 = st.scb[m][4 * h] | (st.scb[m][4 * h + 1] << 8) | (st.scb[m][4 * h + 2] << 16) | (st.scb[m][4 * h + 3] << 24);
+          fp8x4(w4, sf[m]);
+        }
       }
       f32x4 part[MT][NM];
 #pragma unroll
@@ -379,7 +451,10 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
       if constexpr (SB == 4) {
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
-          const float f = fp8x1((st.sc[m][0] >> (8 * h)) & 0xFFu);
+          uint32_t c;
+          if constexpr (KF) c = (st.scw[m] >> (8 * h)) & 0xFFu;
+          else c = st.scb[m][h];
+          const float f = fp8x1(c);
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) acc[mt][m] += part[mt][m] * f;
         }
@@ -400,9 +475,11 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
     }
   };
 
-  // partial-sum exchange of items split between workgroups (per wave, no workgroup barrier)
+  // partial-sum exchange of items split between workgroups (per wave, no workgroup barrier).
+  // A workgroup holds at most two split items, the first and the last of its range: their
+  // partial tiles are stored (device-coherent) when the item's part ends, and the arrival
+  // counts and sums wait for the end of the range, where they hold up no streaming.
   const int64_t npart_floats = G * 2 * kWaves * PF;
-  const __amdgpu_buffer_rsrc_t rp = buffer_rsrc(a.part, npart_floats * 4);
   auto part_off = [&](int64_t gg, int which, int mt, int m) {   // byte offset of this lane's float4
     return (int)((((gg * 2 + which) * kWaves + wave) * PF + (mt * NM + m) * kWave * 4 + lane * 4) * 4);
   };
@@ -411,46 +488,8 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
     return min(min(slots[r0], slots[r0 + 1]), min(slots[r0 + 2], slots[r0 + 3])) < a.num_slots;
   };
 
-  // epilogue of one item (reference order: acc * es; silu(g) * (u * es_u); * topk weight)
-  auto epilogue = [&](const Pos& p, int b, bool full, bool first) {
-    if (!full) {
-      const int64_t it = (pm0 + p.pm) * nrt + p.pn;
-      const int g_lo = owner(it * nun, U, G), g_hi = owner(it * nun + nun - 1, U, G);
-      const int which = first ? 0 : 1;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        if (!real_rows(b, mt)) continue;
-#pragma unroll
-        for (int m = 0; m < NM; ++m)
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[mt][m]), rp, part_off(g, which, mt, m),
-                                                 0, kCohere);
-      }
-      __builtin_amdgcn_s_waitcnt(0);     // the partial is visible device-wide before the count
-      int32_t* cnt = a.counters + it * kWaves + wave;
-      int old = 0;
-      if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      old = __builtin_amdgcn_readlane(old, 0);
-      if (old != g_hi - g_lo) return;    // another workgroup finishes this item
-      if (lane == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      // sum the parts in workgroup order
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        if (!real_rows(b, mt)) continue;
-#pragma unroll
-        for (int m = 0; m < NM; ++m) {
-          f32x4 t = acc[mt][m];
-          for (int gg = g_lo; gg <= g_hi; ++gg) {
-            f32x4 v = acc[mt][m];
-            if (gg != g) {
-              const int w = (U * gg / G) / nun == it ? 0 : 1;
-              v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, part_off(gg, w, mt, m), 0, kCohere));
-            }
-            t = gg == g_lo ? v : t + v;
-          }
-          acc[mt][m] = t;
-        }
-      }
-    }
+  // stores of one finished item (reference order: acc * es; silu(g) * (u * es_u); * topk weight)
+  auto store_item = [&](const Pos& p, int b) {
     const int nrow = p.pn * kRows + wave * 16 + ln;
     if (nrow >= a.N) return;
     const float es0 = blk_es[b][0], es1 = blk_es[b][NM - 1];
@@ -471,11 +510,71 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
         }
       }
   };
+  Pos split_p0{0, 0, 0}, split_p1{0, 0, 0};
+  int split_b0 = 0, split_b1 = 0, n_split = 0;
+  auto end_item = [&](const Pos& p, int b, bool full, bool first) {
+    if (full) {
+      store_item(p, b);
+      return;
+    }
+    const __amdgpu_buffer_rsrc_t rp = buffer_rsrc(a.part, npart_floats * 4);
+    const int which = first ? 0 : 1;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      if (!real_rows(b, mt)) continue;
+#pragma unroll
+      for (int m = 0; m < NM; ++m)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[mt][m]), rp, part_off(g, which, mt, m), 0,
+                                               kCohere);
+    }
+    if (n_split == 0) {                // (named slots, not an indexed array: no scratch memory)
+      split_p0 = p;
+      split_b0 = b;
+    } else {
+      split_p1 = p;
+      split_b1 = b;
+    }
+    ++n_split;
+  };
+  auto finish_splits = [&]() {
+    if (n_split == 0) return;
+    const __amdgpu_buffer_rsrc_t rp = buffer_rsrc(a.part, npart_floats * 4);
+    __builtin_amdgcn_s_waitcnt(0);       // this wave's partials are visible device-wide before the counts
+    for (int k = 0; k < n_split; ++k) {
+      const Pos p = k == 0 ? split_p0 : split_p1;
+      const int b = k == 0 ? split_b0 : split_b1;
+      const int64_t it = (pm0 + p.pm) * nrt + p.pn;
+      const int g_lo = owner(it * nun, U, G), g_hi = owner(it * nun + nun - 1, U, G);
+      int32_t* cnt = a.counters + it * kWaves + wave;
+      int old = 0;
+      if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      old = __builtin_amdgcn_readlane(old, 0);
+      if (old != g_hi - g_lo) continue;  // another workgroup finishes this item
+      if (lane == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // sum the parts in workgroup order
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        if (!real_rows(b, mt)) continue;
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+          f32x4 t = f32x4{0.f, 0.f, 0.f, 0.f};
+          for (int gg = g_lo; gg <= g_hi; ++gg) {
+            const int w = (U * gg / G) / nun == it ? 0 : 1;
+            const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, part_off(gg, w, mt, m), 0,
+                                                                                             kCohere));
+            t = gg == g_lo ? v : t + v;
+          }
+          acc[mt][m] = t;
+        }
+      }
+      store_item(p, b);
+    }
+  };
 
   // ---- prologue: descriptors and the first trip's loads in flight, then the rest of the staging
   Pos cp{0, (int)(item0 - pm0 * nrt), (int)(ub - item0 * nun)};
   Pos lp = cp;
-  Stage<BITS, MT, NM, SB> st[P];
+  Stage<BITS, NM, SB, KF> st[P];
   int jl = 0;
   setup(lp);
 #pragma unroll
@@ -501,22 +600,30 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
   }
   // (the first trip's barrier below also publishes these)
 
-  // ---- main loop: one trip of P units per iteration, one barrier per trip
+  // ---- main loop: one trip of P units per iteration, one barrier per trip.
+  // Load order per trip: [activation tiles of the next trip: AT] then per unit [weights of the
+  // unit P ahead: WU]. Hence: the trip's own tiles have P * WU loads after them, and a unit's
+  // weights have (P - 1) * WU + AT.
   int cur_e = -1, cur_b = -1, e = -1, sa = 0;
   bool first = true;
   for (int j0 = 0; j0 < n; j0 += P) {
     uint32_t* tiles = ring[(j0 / P) & 1];
+    vm_wait<P * WU>(ax[0][0][0]);
 #pragma unroll
     for (int d = 0; d < P; ++d)
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) tiles[(d * 2 + h) * TILE + mt * 1024 + wave * 64 + lane] = ax[d][h][mt];
+        for (int mt = 0; mt < MT; ++mt) {
+          if (d + h + mt > 0) after_wait(ax[d][h][mt]);
+          tiles[(d * 2 + h) * TILE + mt * 1024 + wave * 64 + lane] = ax[d][h][mt];
+        }
     act_trip();
     __syncthreads();                   // the trip's tiles are complete; the previous trip's readers are done
 #pragma unroll
     for (int d = 0; d < P; ++d) {
       const int j = j0 + d;
+      wait_stage(std::integral_constant<int, (P - 1) * WU + AT>{}, st[d]);
       if (j < n) {
         const int b = min(cp.pm, MAXBLK - 1);
         if (b != cur_b) {                // a new block: its expert and pair tables
@@ -539,7 +646,7 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
         }
         if (e >= 0) {
           compute(cp.s, st[d], tiles + d * 2 * TILE);
-          if (cp.s == nun - 1 || j == n - 1) epilogue(cp, b, sa == 0 && cp.s == nun - 1, first);
+          if (cp.s == nun - 1 || j == n - 1) end_item(cp, b, sa == 0 && cp.s == nun - 1, first);
         }
         advance(cp);
       }
@@ -549,6 +656,8 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
       ++jl;
     }
   }
+  finish_splits();
+  __builtin_amdgcn_s_waitcnt(0);       // no load of this wave is left in flight at exit
 }
 
 // ----------------------------------------------------------------------------------- reduction
@@ -583,7 +692,8 @@ __global__ __launch_bounds__(256) void moe_reduce_kernel(const float* __restrict
 
 template <int BITS, int ADT, bool GLU, int MT>
 static void launch_sb(int sb, dim3 grid, hipStream_t st, const MoeArgs& a) {
-  const bool kf = (a.K / kHexBlock) % 8 == 0;     // whole 256-input units: no tail checks
+  // whole 256-input units with aligned scale rows: no tail checks, one load per unit's scales
+  const bool kf = (a.K / kHexBlock) % 8 == 0 && a.scale_words;
   const dim3 block(kThreads);
   if (sb == 1) {
     if (kf) hipLaunchKernelGGL((hex_moe_kernel<BITS, ADT, GLU, MT, 1, true>), grid, block, 0, st, a);
