@@ -106,60 +106,42 @@ struct Stage {
   uint32_t scb[NM][KF ? 1 : (SB == 1 ? 8 : 2)];
 };
 
-// Buffer descriptors of the weight stream's current item, as four SGPRs each (the hot loop's
-// loads are hand-scheduled, below). Each spans one expert's matrix, so loads past its end return
+// Buffer descriptors of the weight stream's current item. Each spans one expert's matrix, so loads past its end return
 // zero instead of faulting; rows past the matrix read out of range (nothing fetched) and are
 // never stored. The unit offset goes in the scalar soffset.
 template <int NM>
 struct ItemRes {
-  u32x4 rw[NM];          // packed index words of the item's expert
-  u32x4 rb[NM];          // its fp8 block scales
-  int vw[NM], vb[NM];    // lane offsets: row n, block lane / 16 of the unit
+  __amdgpu_buffer_rsrc_t rw[NM];   // packed index words of the item's expert
+  __amdgpu_buffer_rsrc_t rb[NM];   // its fp8 block scales
+  int vw[NM], vb[NM];              // lane offsets: row n, block lane / 16 of the unit
 };
 
-// Hand-scheduled buffer loads. The compiler does not see these as memory operations, so it
-// inserts no waits for them; the kernel waits with explicit s_waitcnt vmcnt(N) whose operands
-// are the loaded registers (so no use can move above the wait). N counts the loads issued after
-// the awaited ones in program order; any other memory operation issued in between only makes
-// the wait stricter, so conditional stores cannot break it.
-__device__ __forceinline__ u32x4 make_desc(const void* base, int64_t bytes) {
-  const uint64_t p = reinterpret_cast<uint64_t>(base);
-  const uint32_t n = (uint32_t)(bytes > 0x7FFFFFFF ? 0x7FFFFFFF : bytes);
-  return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)p),
-               (uint32_t)__builtin_amdgcn_readfirstlane((int)((uint32_t)(p >> 32) & 0xFFFFu)),
-               (uint32_t)__builtin_amdgcn_readfirstlane((int)n), 0x00020000u};
+// Buffer loads of the hot loop. They go through the compiler's buffer builtins, so the
+// compiler tracks each one and waits for exactly the loads a use needs; the loop keeps every
+// load unconditional and in a fixed order, so those waits stay partial (vmcnt(N), not 0).
+template <int IMM>
+__device__ __forceinline__ void ld_x4(u32x4& d, __amdgpu_buffer_rsrc_t r, int v) {
+  d = __builtin_amdgcn_raw_buffer_load_b128(r, v + IMM, 0, 0);
 }
 template <int IMM>
-__device__ __forceinline__ void ld_x4(u32x4& d, const u32x4& r, int v, int s) {
-  asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen offset:%4" : "=v"(d) : "v"(v), "s"(r), "s"(s), "i"(IMM));
+__device__ __forceinline__ void ld_x3(u32x3& d, __amdgpu_buffer_rsrc_t r, int v) {
+  d = __builtin_amdgcn_raw_buffer_load_b96(r, v + IMM, 0, 0);
 }
 template <int IMM>
-__device__ __forceinline__ void ld_x3(u32x3& d, const u32x4& r, int v, int s) {
-  asm volatile("buffer_load_dwordx3 %0, %1, %2, %3 offen offset:%4" : "=v"(d) : "v"(v), "s"(r), "s"(s), "i"(IMM));
+__device__ __forceinline__ void ld_x2(u32x2& d, __amdgpu_buffer_rsrc_t r, int v) {
+  d = __builtin_amdgcn_raw_buffer_load_b64(r, v + IMM, 0, 0);
 }
 template <int IMM>
-__device__ __forceinline__ void ld_x2(u32x2& d, const u32x4& r, int v, int s) {
-  asm volatile("buffer_load_dwordx2 %0, %1, %2, %3 offen offset:%4" : "=v"(d) : "v"(v), "s"(r), "s"(s), "i"(IMM));
+__device__ __forceinline__ void ld_x1(uint32_t& d, __amdgpu_buffer_rsrc_t r, int v) {
+  d = __builtin_amdgcn_raw_buffer_load_b32(r, v + IMM, 0, 0);
 }
 template <int IMM>
-__device__ __forceinline__ void ld_x1(uint32_t& d, const u32x4& r, int v, int s) {
-  asm volatile("buffer_load_dword %0, %1, %2, %3 offen offset:%4" : "=v"(d) : "v"(v), "s"(r), "s"(s), "i"(IMM));
+__device__ __forceinline__ void ld_u16(uint32_t& d, __amdgpu_buffer_rsrc_t r, int v) {
+  d = __builtin_amdgcn_raw_buffer_load_b16(r, v + IMM, 0, 0);
 }
 template <int IMM>
-__device__ __forceinline__ void ld_u16(uint32_t& d, const u32x4& r, int v, int s) {
-  asm volatile("buffer_load_ushort %0, %1, %2, %3 offen offset:%4" : "=v"(d) : "v"(v), "s"(r), "s"(s), "i"(IMM));
-}
-template <int IMM>
-__device__ __forceinline__ void ld_u8(uint32_t& d, const u32x4& r, int v, int s) {
-  asm volatile("buffer_load_ubyte %0, %1, %2, %3 offen offset:%4" : "=v"(d) : "v"(v), "s"(r), "s"(s), "i"(IMM));
-}
-template <int N, typename T>
-__device__ __forceinline__ void vm_wait(T& x) {      // wait until at most N loads are outstanding
-  asm volatile("s_waitcnt vmcnt(%1)" : "+v"(x) : "i"(N));
-}
-template <typename T>
-__device__ __forceinline__ void after_wait(T& x) {   // order x's uses after the wait just above
-  asm volatile("" : "+v"(x));
+__device__ __forceinline__ void ld_u8(uint32_t& d, __amdgpu_buffer_rsrc_t r, int v) {
+  d = __builtin_amdgcn_raw_buffer_load_b8(r, v + IMM, 0, 0);
 }
 
 constexpr int kRsrcWord3 = 0x00020000;   // raw buffer, 32-bit data format (gfx9 family)
@@ -178,7 +160,6 @@ constexpr int kMaxExperts = 1024;        // global expert ids the tier lookup ma
 constexpr int kThreads = 1024;           // 16 waves, one workgroup per compute unit
 constexpr int kWaves = kThreads / kWave;
 constexpr int kRows = 16 * kWaves;       // output rows of one work item: 16 per wave
-constexpr int kUnitIn = 256;             // inputs per unit: two 128-input steps
 constexpr int kMinUnits = 2;             // units per workgroup below which the grid shrinks
 
 // Units per trip P: the weight loads of P units are in flight per wave ahead of the math, and
@@ -287,16 +268,14 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
       const bh_hex_proj& w = m == 0 ? a.w0 : a.w1;
-      R.rw[m] = make_desc(w.idx + ee * w.s_ie, (int64_t)a.N * w.s_in * 4);
-      R.rb[m] = make_desc(w.block_scale + ee * w.s_be, (int64_t)a.N * w.s_bn);
+      R.rw[m] = buffer_rsrc(w.idx + ee * w.s_ie, (int64_t)a.N * w.s_in * 4);
+      R.rb[m] = buffer_rsrc(w.block_scale + ee * w.s_be, (int64_t)a.N * w.s_bn);
       R.vw[m] = rv ? (int)(nrow * w.s_in * 4) + lg * BLKB : kOOR;
       R.vb[m] = rv ? (int)(nrow * w.s_bn) : kOOR;
     }
   };
   // loads of unit s of the current descriptors; dummy units (past the range) read out of range.
-  // WU loads per unit, in this order: per matrix the two steps' blocks, then its scales.
-  constexpr int SCN = KF ? 1 : (SB == 1 ? 8 : 2);
-  constexpr int WU = NM * (2 + SCN);
+  // per matrix: the two steps' blocks, then the unit's scales
   // The whole byte offset goes in the range-checked VGPR offset (soffset 0): dummy units and
   // invalid rows sit past every resource.
   auto load = [&](int s_, bool real, Stage<BITS, NM, SB, KF>& st) {
@@ -307,49 +286,32 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
     for (int m = 0; m < NM; ++m) {
       const int vw = R.vw[m] + ws, vb = R.vb[m] + bs;
       if constexpr (BITS == 4) {
-        ld_x4<0>(st.w[m][0], R.rw[m], vw, 0);
-        ld_x4<4 * BLKB>(st.w[m][1], R.rw[m], vw, 0);
+        ld_x4<0>(st.w[m][0], R.rw[m], vw);
+        ld_x4<4 * BLKB>(st.w[m][1], R.rw[m], vw);
       } else {
-        ld_x3<0>(st.w[m][0], R.rw[m], vw, 0);
-        ld_x3<4 * BLKB>(st.w[m][1], R.rw[m], vw, 0);
+        ld_x3<0>(st.w[m][0], R.rw[m], vw);
+        ld_x3<4 * BLKB>(st.w[m][1], R.rw[m], vw);
       }
       if constexpr (KF) {
-        if constexpr (SB == 1) ld_x2<0>(st.scw[m], R.rb[m], vb, 0);
-        else ld_u16<0>(st.scw[m], R.rb[m], vb, 0);
+        if constexpr (SB == 1) ld_x2<0>(st.scw[m], R.rb[m], vb);
+        else ld_u16<0>(st.scw[m], R.rb[m], vb);
       } else {
-        ld_u8<0>(st.scb[m][0], R.rb[m], vb, 0);
-        ld_u8<1>(st.scb[m][1], R.rb[m], vb, 0);
+        ld_u8<0>(st.scb[m][0], R.rb[m], vb);
+        ld_u8<1>(st.scb[m][1], R.rb[m], vb);
         if constexpr (SB == 1) {
-          ld_u8<2>(st.scb[m][2], R.rb[m], vb, 0);
-          ld_u8<3>(st.scb[m][3], R.rb[m], vb, 0);
-          ld_u8<4>(st.scb[m][4], R.rb[m], vb, 0);
-          ld_u8<5>(st.scb[m][5], R.rb[m], vb, 0);
-          ld_u8<6>(st.scb[m][6], R.rb[m], vb, 0);
-          ld_u8<7>(st.scb[m][7], R.rb[m], vb, 0);
+          ld_u8<2>(st.scb[m][2], R.rb[m], vb);
+          ld_u8<3>(st.scb[m][3], R.rb[m], vb);
+          ld_u8<4>(st.scb[m][4], R.rb[m], vb);
+          ld_u8<5>(st.scb[m][5], R.rb[m], vb);
+          ld_u8<6>(st.scb[m][6], R.rb[m], vb);
+          ld_u8<7>(st.scb[m][7], R.rb[m], vb);
         }
       }
     }
   };
-  // wait for a stage's loads, with N later loads allowed in flight
-  auto wait_stage = [&](auto n_later, Stage<BITS, NM, SB, KF>& st) {
-    constexpr int N = decltype(n_later)::value;
-    vm_wait<N>(st.w[0][0]);
-#pragma unroll
-    for (int m = 0; m < NM; ++m) {
-      if (m > 0) after_wait(st.w[m][0]);
-      after_wait(st.w[m][1]);
-      if constexpr (KF) {
-        after_wait(st.scw[m]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < SCN; ++i) after_wait(st.scb[m][i]);
-      }
-    }
-  };
-
   // ---- activation stream: the tiles of the next trip, one dword per lane per (unit, step, subtile)
   const int x_rows = (int)((a.num_slots + a.a_div - 1) / a.a_div);
-  const u32x4 rx = make_desc(a.x, (int64_t)x_rows * a.s_xm * 2);
+  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(a.x, (int64_t)x_rows * a.s_xm * 2);
   // lane dword of a step's tile: wave w, lane l -> slot l / 4 of the subtile, inputs
   // 32 (w / 4) + 8 (w % 4) + 2 (l % 4) of the step (the fragment layout the MFMA reads)
   const int xcol = (wave >> 2) * 64 + (wave & 3) * 16 + (lane & 3) * 4;
@@ -363,7 +325,6 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
       vx[mt] = (e >= 0 && slot < a.num_slots) ? (int)((int64_t)(slot / a.a_div) * a.s_xm * 2) + xcol : kOOR;
     }
   };
-  constexpr int AT = P * 2 * MT;                 // activation loads per trip
   uint32_t ax[P][2][MT];
   Pos ap{0, (int)(item0 - pm0 * nrt), (int)(ub - item0 * nun)};
   int ja = 0;
@@ -389,7 +350,7 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) ld_x1<0>(ax[d][h][mt], rx, vxd[d][mt] + xs[d][h], 0);
+        for (int mt = 0; mt < MT; ++mt) ld_x1<0>(ax[d][h][mt], rx, vxd[d][mt] + xs[d][h]);
   };
 
   // ---- compute stream
@@ -571,20 +532,9 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
     }
   };
 
-  // ---- prologue: descriptors and the first trip's loads in flight, then the rest of the staging
-  Pos cp{0, (int)(item0 - pm0 * nrt), (int)(ub - item0 * nun)};
-  Pos lp = cp;
-  Stage<BITS, NM, SB, KF> st[P];
-  int jl = 0;
-  setup(lp);
-#pragma unroll
-  for (int d = 0; d < P; ++d) {
-    if (d > 0 && lp.s == 0 && jl < n) setup(lp);
-    load(lp.s, jl < n, st[d]);
-    advance(lp);
-    ++jl;
-  }
-  act_trip();
+  // ---- prologue: the rest of the staging, then the pipeline's first loads in the loop's order
+  // (activation tiles, then weights), so the compiler sees one load order on both paths into the
+  // loop and keeps its waits partial
   for (int b = tid; b < MAXBLK; b += kThreads) {
     const int e = expert_of(b);
     blk_e[b] = e;
@@ -599,31 +549,42 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
     blk_lv[b][m][c] = e >= 0 ? (uint16_t)to_bits<ADT>((m == 0 ? a.w0 : a.w1).levels[(int64_t)e * L + c]) : 0;
   }
   // (the first trip's barrier below also publishes these)
+  Pos cp{0, (int)(item0 - pm0 * nrt), (int)(ub - item0 * nun)};
+  Pos lp = cp;
+  Stage<BITS, NM, SB, KF> st[P];
+  int jl = 0;
+  setup(lp);
+  __builtin_amdgcn_sched_barrier(0);
+  act_trip();
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int d = 0; d < P; ++d) {
+    if (d > 0 && lp.s == 0 && jl < n) setup(lp);
+    load(lp.s, jl < n, st[d]);
+    advance(lp);
+    ++jl;
+  }
+  __builtin_amdgcn_sched_barrier(0);
 
-  // ---- main loop: one trip of P units per iteration, one barrier per trip.
-  // Load order per trip: [activation tiles of the next trip: AT] then per unit [weights of the
-  // unit P ahead: WU]. Hence: the trip's own tiles have P * WU loads after them, and a unit's
-  // weights have (P - 1) * WU + AT.
+  // ---- main loop: one trip of P units per iteration, one barrier per trip. Loads per trip, in
+  // order: the next trip's activation tiles, then per unit the weights of the unit P ahead.
   int cur_e = -1, cur_b = -1, e = -1, sa = 0;
   bool first = true;
   for (int j0 = 0; j0 < n; j0 += P) {
     uint32_t* tiles = ring[(j0 / P) & 1];
-    vm_wait<P * WU>(ax[0][0][0]);
 #pragma unroll
     for (int d = 0; d < P; ++d)
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          if (d + h + mt > 0) after_wait(ax[d][h][mt]);
-          tiles[(d * 2 + h) * TILE + mt * 1024 + wave * 64 + lane] = ax[d][h][mt];
-        }
+        for (int mt = 0; mt < MT; ++mt) tiles[(d * 2 + h) * TILE + mt * 1024 + wave * 64 + lane] = ax[d][h][mt];
+    __builtin_amdgcn_sched_barrier(0);   // (no load moves across: the load order above is the waits' premise)
     act_trip();
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();                   // the trip's tiles are complete; the previous trip's readers are done
 #pragma unroll
     for (int d = 0; d < P; ++d) {
       const int j = j0 + d;
-      wait_stage(std::integral_constant<int, (P - 1) * WU + AT>{}, st[d]);
       if (j < n) {
         const int b = min(cp.pm, MAXBLK - 1);
         if (b != cur_b) {                // a new block: its expert and pair tables
@@ -651,7 +612,9 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
         advance(cp);
       }
       if (lp.s == 0 && jl < n) setup(lp);
+      __builtin_amdgcn_sched_barrier(0);
       load(lp.s, jl < n, st[d]);
+      __builtin_amdgcn_sched_barrier(0);
       advance(lp);
       ++jl;
     }
