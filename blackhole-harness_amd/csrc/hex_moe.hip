@@ -57,7 +57,7 @@ struct MoeArgs {
   int32_t scale_words;   // block_scale rows allow one load of a unit's scales (8 or 2 bytes)
                          // (host only: it selects the whole-unit kernel variant)
   float* part;           // workspace: partial sums of items split between workgroups
-  int32_t* counters;     // workspace: arrivals per (item, wave), zero between calls
+  int32_t* counters;     // workspace: arrivals per split item (64 bytes apart), zero between calls
 };
 
 // Four fp8 scales (one byte each) -> float, by the conversion instruction; a wave holding a
@@ -209,6 +209,7 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
   __shared__ int blk_e[MAXBLK];                                    // its tier-local expert, -1 for none
   __shared__ float blk_es[MAXBLK][NM];                             // expert scales
   __shared__ uint16_t blk_lv[MAXBLK][NM][L];                       // levels in the activation dtype
+  __shared__ int split_last[2];                                    // this workgroup finishes split item k
 
   const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, lg = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: units and row tiles stay scalar
@@ -497,21 +498,38 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
     }
     ++n_split;
   };
+  // One counter per split item, on its own 64-byte line (kWaves ints apart), bumped once per
+  // workgroup after a barrier: every wave's partial tile is out before the count.
   auto finish_splits = [&]() {
-    if (n_split == 0) return;
+    if (n_split == 0) return;            // (uniform: all waves share the range)
+    __builtin_amdgcn_s_waitcnt(0);       // this wave's partial tiles are visible device-wide
+    __syncthreads();                     // ... and every wave's
+    int64_t it[2];
+    int g_lo[2], g_hi[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const Pos p = k == 0 ? split_p0 : split_p1;
+      it[k] = (pm0 + p.pm) * nrt + p.pn;
+      g_lo[k] = owner(it[k] * nun, U, G);
+      g_hi[k] = owner(it[k] * nun + nun - 1, U, G);
+    }
+    if (tid == 0) {                      // both arrivals in flight together
+      int old0 = 0, old1 = 0;
+      old0 = __hip_atomic_fetch_add(a.counters + it[0] * kWaves, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (n_split > 1)
+        old1 = __hip_atomic_fetch_add(a.counters + it[1] * kWaves, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const bool l0 = old0 == g_hi[0] - g_lo[0], l1 = n_split > 1 && old1 == g_hi[1] - g_lo[1];
+      if (l0) __hip_atomic_store(a.counters + it[0] * kWaves, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (l1) __hip_atomic_store(a.counters + it[1] * kWaves, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      split_last[0] = l0;
+      split_last[1] = l1;
+    }
+    __syncthreads();
     const __amdgpu_buffer_rsrc_t rp = buffer_rsrc(a.part, npart_floats * 4);
-    __builtin_amdgcn_s_waitcnt(0);       // this wave's partials are visible device-wide before the counts
     for (int k = 0; k < n_split; ++k) {
+      if (!split_last[k]) continue;      // another workgroup finishes this item
       const Pos p = k == 0 ? split_p0 : split_p1;
       const int b = k == 0 ? split_b0 : split_b1;
-      const int64_t it = (pm0 + p.pm) * nrt + p.pn;
-      const int g_lo = owner(it * nun, U, G), g_hi = owner(it * nun + nun - 1, U, G);
-      int32_t* cnt = a.counters + it * kWaves + wave;
-      int old = 0;
-      if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      old = __builtin_amdgcn_readlane(old, 0);
-      if (old != g_hi - g_lo) continue;  // another workgroup finishes this item
-      if (lane == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       // sum the parts in workgroup order
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
@@ -519,11 +537,11 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
           f32x4 t = f32x4{0.f, 0.f, 0.f, 0.f};
-          for (int gg = g_lo; gg <= g_hi; ++gg) {
-            const int w = (U * gg / G) / nun == it ? 0 : 1;
+          for (int gg = g_lo[k]; gg <= g_hi[k]; ++gg) {
+            const int w = (U * gg / G) / nun == it[k] ? 0 : 1;
             const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, part_off(gg, w, mt, m), 0,
                                                                                              kCohere));
-            t = gg == g_lo ? v : t + v;
+            t = gg == g_lo[k] ? v : t + v;
           }
           acc[mt][m] = t;
         }
@@ -711,8 +729,8 @@ static int64_t moe_grid(int64_t num_blocks, int64_t n_out, int64_t n_in, int mt)
   return g > 0 ? g : 1;
 }
 
-// Workspace of one launch: arrival counters (one per item and wave) and partial-sum tiles (two
-// per workgroup and wave), as two separate buffers so calls of any shape can share them.
+// Workspace of one launch: arrival counters (one per item, 64 bytes apart) and partial-sum tiles
+// (two per workgroup and wave), as two separate buffers so calls of any shape can share them.
 struct Workspace {
   int64_t counters, partials;      // int32 counters, float partials
 };
