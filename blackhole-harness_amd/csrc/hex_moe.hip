@@ -550,9 +550,9 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
     }
   };
 
-  // ---- prologue: the rest of the staging, then the pipeline's first loads in the loop's order
-  // (activation tiles, then weights), so the compiler sees one load order on both paths into the
-  // loop and keeps its waits partial
+  // ---- prologue: the rest of the staging (its waits leave nothing in flight), then the
+  // pipeline's first loads in the loop's order: activation tiles, weights, and the first trip's
+  // tiles published
   for (int b = tid; b < MAXBLK; b += kThreads) {
     const int e = expert_of(b);
     blk_e[b] = e;
@@ -566,12 +566,19 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
     const int e = expert_of(b);
     blk_lv[b][m][c] = e >= 0 ? (uint16_t)to_bits<ADT>((m == 0 ? a.w0 : a.w1).levels[(int64_t)e * L + c]) : 0;
   }
-  // (the first trip's barrier below also publishes these)
   Pos cp{0, (int)(item0 - pm0 * nrt), (int)(ub - item0 * nun)};
   Pos lp = cp;
   Stage<BITS, NM, SB, KF> st[P];
   int jl = 0;
   setup(lp);
+  auto publish = [&](uint32_t* tiles) {        // this trip's activation tiles into the ring
+#pragma unroll
+    for (int d = 0; d < P; ++d)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) tiles[(d * 2 + h) * TILE + mt * 1024 + wave * 64 + lane] = ax[d][h][mt];
+  };
   __builtin_amdgcn_sched_barrier(0);
   act_trip();
   __builtin_amdgcn_sched_barrier(0);
@@ -583,23 +590,20 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
     ++jl;
   }
   __builtin_amdgcn_sched_barrier(0);
+  publish(ring[0]);
+  __builtin_amdgcn_sched_barrier(0);
+  act_trip();
+  __builtin_amdgcn_sched_barrier(0);
+  __syncthreads();                     // the first trip's tiles and the staged plan are complete
 
-  // ---- main loop: one trip of P units per iteration, one barrier per trip. Loads per trip, in
-  // order: the next trip's activation tiles, then per unit the weights of the unit P ahead.
+  // ---- main loop: one trip of P units per iteration. Loads per trip, in order: per unit the
+  // weights of the unit P ahead, then the activation tiles of the trip after next. The next
+  // trip's tiles go into the other ring stage at the end, under one barrier per trip.
   int cur_e = -1, cur_b = -1, e = -1, sa = 0;
   bool first = true;
   for (int j0 = 0; j0 < n; j0 += P) {
-    uint32_t* tiles = ring[(j0 / P) & 1];
-#pragma unroll
-    for (int d = 0; d < P; ++d)
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) tiles[(d * 2 + h) * TILE + mt * 1024 + wave * 64 + lane] = ax[d][h][mt];
-    __builtin_amdgcn_sched_barrier(0);   // (no load moves across: the load order above is the waits' premise)
-    act_trip();
-    __builtin_amdgcn_sched_barrier(0);
-    __syncthreads();                   // the trip's tiles are complete; the previous trip's readers are done
+    const int t = j0 / P;
+    const uint32_t* tiles = ring[t & 1];
 #pragma unroll
     for (int d = 0; d < P; ++d) {
       const int j = j0 + d;
@@ -636,6 +640,11 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
       advance(lp);
       ++jl;
     }
+    publish(ring[(t + 1) & 1]);        // (its readers, two trips back, passed the last barrier)
+    __builtin_amdgcn_sched_barrier(0);
+    act_trip();
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();                   // the next trip's tiles are complete
   }
   finish_splits();
   __builtin_amdgcn_s_waitcnt(0);       // no load of this wave is left in flight at exit
