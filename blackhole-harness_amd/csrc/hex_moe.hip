@@ -220,10 +220,12 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
   // ---- this workgroup's contiguous range of units over the used blocks
   const int64_t used = (int64_t)a.npp[0] / BM;
   const int64_t U = used * nrt * nun;
-  // With no more items than workgroups each workgroup takes one whole item: no item is split,
-  // so no partial sums are exchanged. Otherwise the units are spread evenly (no empty range).
+  // With between half and all as many items as workgroups, each workgroup takes one whole item:
+  // no item is split, so no partial sums are exchanged. Otherwise the units are spread evenly
+  // (no empty range), splitting items.
   const int64_t items = used * nrt;
-  const int64_t G = items <= (int64_t)gridDim.x ? items : min((int64_t)gridDim.x, U), g = blockIdx.x;
+  const bool whole = items <= (int64_t)gridDim.x && 2 * items >= (int64_t)gridDim.x;
+  const int64_t G = whole ? items : min((int64_t)gridDim.x, U), g = blockIdx.x;
   if (g >= G) return;
   const int64_t ub = U * g / G, ue = U * (g + 1) / G;
   const int n = (int)(ue - ub);
