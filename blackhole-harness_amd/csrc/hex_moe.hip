@@ -361,69 +361,80 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
 
   // ---- compute stream
   f32x4 acc[MT][NM];
+  // One unit = 8 MFMA k-slices (2 steps x 4 blocks). The table reads and the activation fragment
+  // of slice k + 1 are issued before the MFMAs of slice k, so LDS latency hides behind them.
   auto compute = [&](int s, const Stage<BITS, NM, SB, KF>& st, const uint32_t* tiles) {
+    uint32_t r[2][NM][4];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      uint32_t r[NM][4];
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int m = 0; m < NM; ++m) {
         if constexpr (BITS == 4) {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) r[m][j] = st.w[m][h][j];
+          for (int j = 0; j < 4; ++j) r[h][m][j] = st.w[m][h][j];
         } else {   // the block's 96-bit stream as four 24-bit fields of 8 codes
-          r[m][0] = st.w[m][h][0];
-          r[m][1] = __builtin_amdgcn_alignbit(st.w[m][h][1], st.w[m][h][0], 24);
-          r[m][2] = __builtin_amdgcn_alignbit(st.w[m][h][2], st.w[m][h][1], 16);
-          r[m][3] = st.w[m][h][2] >> 8;
+          r[h][m][0] = st.w[m][h][0];
+          r[h][m][1] = __builtin_amdgcn_alignbit(st.w[m][h][1], st.w[m][h][0], 24);
+          r[h][m][2] = __builtin_amdgcn_alignbit(st.w[m][h][2], st.w[m][h][1], 16);
+          r[h][m][3] = st.w[m][h][2] >> 8;
         }
-        transpose_rows4(r[m]);     // r[m][q] = field lg of block 8 s + 4 h + q
+        transpose_rows4(r[h][m]);  // r[h][m][q] = field lg of block 8 s + 4 h + q
       }
-      const int nq = KF ? 4 : min(4, nb32 - 8 * s - 4 * h);
-      float sf[NM][4];
-      if constexpr (SB == 1) {
+    const int nk = KF ? 8 : min(8, nb32 - 8 * s);   // valid k-slices of this unit
+    u32x4 bq[2][NM], av[2][MT];
+    auto fetch = [&](int k, int slot) {
 #pragma unroll
-        for (int m = 0; m < NM; ++m) {
-          uint32_t w4;
-          if constexpr (KF) w4 = st.scw[m][h];
-          else w4 = st.scb[m][4 * h] | (st.scb[m][4 * h + 1] << 8) | (st.scb[m][4 * h + 2] << 16) | (st.scb[m][4 * h + 3] << 24);
-          fp8x4(w4, sf[m]);
-        }
-      }
-      f32x4 part[MT][NM];
+      for (int m = 0; m < NM; ++m) bq[slot][m] = lookup8<BITS>(r[k >> 2][m][k & 3], cb[m], tab);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
+        av[slot][mt] = *reinterpret_cast<const u32x4*>(tiles + (k >> 2) * TILE + mt * 1024 + (k & 3) * 256 + lane * 4);
+    };
+    f32x4 part[MT][NM];
+    float sf[NM][4];                 // B = 32: the step's 4 block scales
+    fetch(0, 0);
 #pragma unroll
-        for (int m = 0; m < NM; ++m) part[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < 8; ++k) {
+      const int h = k >> 2, q = k & 3;
+      if (q == 0) {
+        if constexpr (SB == 1) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (q < nq) {
-          u32x4 bq[NM];
-#pragma unroll
-          for (int m = 0; m < NM; ++m) bq[m] = lookup8<BITS>(r[m][q], cb[m], tab);
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) {
-            const u32x4 av = *reinterpret_cast<const u32x4*>(tiles + h * TILE + mt * 1024 + q * 256 + lane * 4);
-#pragma unroll
-            for (int m = 0; m < NM; ++m) {
-              if constexpr (SB == 1) {
-                const f32x4 pr = mfma16x16x32<ADT>(av, bq[m], f32x4{0.f, 0.f, 0.f, 0.f});
-                acc[mt][m] += pr * sf[m][q];
-              } else {
-                part[mt][m] = mfma16x16x32<ADT>(av, bq[m], part[mt][m]);
-              }
-            }
+          for (int m = 0; m < NM; ++m) {
+            uint32_t w4;
+            if constexpr (KF) w4 = st.scw[m][h];
+            else w4 = st.scb[m][4 * h] | (st.scb[m][4 * h + 1] << 8) | (st.scb[m][4 * h + 2] << 16) | (st.scb[m][4 * h + 3] << 24);
+            fp8x4(w4, sf[m]);
           }
         }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int m = 0; m < NM; ++m) part[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+      if (k + 1 < 8 && (KF || k + 1 < nk)) fetch(k + 1, (k + 1) & 1);
+      if (KF || k < nk) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int m = 0; m < NM; ++m) {
+            if constexpr (SB == 1) {
+              const f32x4 pr = mfma16x16x32<ADT>(av[k & 1][mt], bq[k & 1][m], f32x4{0.f, 0.f, 0.f, 0.f});
+              acc[mt][m] += pr * sf[m][q];
+            } else {
+              part[mt][m] = mfma16x16x32<ADT>(av[k & 1][mt], bq[k & 1][m], part[mt][m]);
+            }
+          }
       }
       if constexpr (SB == 4) {
+        if (q == 3) {
 #pragma unroll
-        for (int m = 0; m < NM; ++m) {
-          uint32_t c;
-          if constexpr (KF) c = (st.scw[m] >> (8 * h)) & 0xFFu;
-          else c = st.scb[m][h];
-          const float f = fp8x1(c);
+          for (int m = 0; m < NM; ++m) {
+            uint32_t c;
+            if constexpr (KF) c = (st.scw[m] >> (8 * h)) & 0xFFu;
+            else c = st.scb[m][h];
+            const float f = fp8x1(c);
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt) acc[mt][m] += part[mt][m] * f;
+            for (int mt = 0; mt < MT; ++mt) acc[mt][m] += part[mt][m] * f;
+          }
         }
       }
     }
