@@ -37,6 +37,7 @@ HEX_BLOCK = 32     # inputs per bit stream (blackhole/anatomy/hex.py:44)
 
 DIRECT_MAX = int(os.environ.get("BLACKHOLE_HEX_DIRECT_MAX", "32"))      # slots (hex_moe.py:260)
 DEQUANT_MIN = int(os.environ.get("BLACKHOLE_HEX_DEQUANT_MIN", "1024"))  # slots (hex_moe.py:261)
+PREFILL_MIN = 64     # slots per expert above which the fused path takes the 128-slot prefill kernels
 
 
 def _n_in(p: dict, bits: int) -> int:
@@ -163,12 +164,18 @@ def plan(ids: torch.Tensor, n: int, block_m: int, mode: str = "auto"):
 
 
 def _tile_from(cfg: dict) -> int:
-    """block_m of a config dict: BLOCK_M (slots per expert block) rounded to 16, 32 or 64. The
-    reference's BLOCK_N, BLOCK_K, num_warps and num_stages have no counterpart here (a work item
-    is always 256 output rows, and the kernels split the inputs between workgroups themselves)
-    and are ignored."""
+    """block_m of a config dict: BLOCK_M (slots per expert block) rounded to 16, 32, 64 or 128
+    (128: the prefill kernels). The reference's BLOCK_N, BLOCK_K, num_warps and num_stages have
+    no counterpart here (the kernels fix their own output tiles and input steps) and are
+    ignored."""
     bm = int(cfg.get("BLOCK_M", 16))
-    return 16 if bm <= 16 else (32 if bm <= 32 else 64)
+    return 16 if bm <= 16 else (32 if bm <= 32 else (64 if bm <= 64 else 128))
+
+
+def _fit_tile(bm: int, n_in: int) -> int:
+    """The prefill kernels (block_m 128) step through the inputs 128 at a time; other widths
+    take the 64-slot decode kernels."""
+    return 64 if bm == 128 and n_in % 128 else bm
 
 
 def default_config(slots: int, n_out: int, n_in: int, glu: bool, n_experts: int = 0) -> dict:
@@ -179,8 +186,8 @@ def default_config(slots: int, n_out: int, n_in: int, glu: bool, n_experts: int 
         bm = _tile_from({"BLOCK_M": int(env.split(",")[0])})
     else:
         per_expert = slots / max(1, n_experts or slots)
-        bm = 16 if per_expert <= 16 else (32 if per_expert <= 48 else 64)
-    return {"BLOCK_M": bm, "BLOCK_N": 256}
+        bm = 16 if per_expert <= 16 else (32 if per_expert <= 48 else (64 if per_expert <= PREFILL_MIN else 128))
+    return {"BLOCK_M": _fit_tile(bm, n_in), "BLOCK_N": 256}
 
 
 # --------------------------------------------------------------------------- fused path
@@ -274,8 +281,8 @@ def hex_moe_fused(x, topk_weights, topk_ids, tiers: list[HexTier], config: dict 
     y = (torch.empty if _covers_all(tiers) else torch.zeros)(S, H, dtype=torch.float32, device=x.device)
     c1 = config or default_config(S, I, H, True, E)
     c2 = config or default_config(S, H, I, False, E)
-    bm1 = _tile_from(c1)
-    bm2 = _tile_from(c2)
+    bm1 = _fit_tile(_tile_from(c1), H)
+    bm2 = _fit_tile(_tile_from(c2), I)
     p1 = plan(flat, E, bm1, align_mode)
     p2 = p1 if bm2 == bm1 else plan(flat, E, bm2, align_mode)
     for t in tiers:

@@ -1,0 +1,155 @@
+// Pieces shared by the fused HEX expert kernels: the launch arguments, fp8 scale decoding,
+// pair-table operand lookup, and raw buffer loads.
+#pragma once
+
+#include "hex_common.h"
+
+namespace bh {
+
+int check_proj(const bh_hex_proj* w, int64_t n_in, const char* who, int* block);
+
+struct MoeArgs {
+  const uint16_t* x;     // activations [rows, K] (bf16/f16 bits)
+  int64_t s_xm;
+  void* out;             // GLU: act [slots, N] (activation dtype); down: y [slots, N] float
+  int64_t s_om;
+  bh_hex_proj w0, w1;    // gate, up (GLU) or down (w0 only)
+  const int32_t* sid;
+  const int32_t* eid;
+  const int32_t* npp;
+  const int32_t* lookup;
+  const float* topk_w;
+  int64_t num_slots;
+  int32_t n_experts;
+  int32_t a_div;
+  int32_t N, K;
+  int32_t scale_words;   // block_scale rows allow one load of a unit's scales (8 or 2 bytes)
+                         // (host only: it selects the whole-unit kernel variant)
+  float* part;           // workspace: partial sums of items split between workgroups
+  int32_t* counters;     // workspace: arrivals per split item (64 bytes apart), zero between calls
+};
+
+// Four fp8 scales (one byte each) -> float, by the conversion instruction; a wave holding a
+// 0x7F / 0xFF code (NaN for the instruction, +-480 for the reference formula) takes the formula.
+__device__ __forceinline__ void fp8x4(uint32_t w, float f[4]) {
+  const bool special = (((w & 0x7F7F7F7Fu) + 0x01010101u) & 0x80808080u) != 0u;
+  if (__builtin_expect(__ballot(special) != 0ull, 0)) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f[j] = fp8_e4m3((w >> (8 * j)) & 0xFFu);
+  } else {
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+    f[0] = lo[0]; f[1] = lo[1]; f[2] = hi[0]; f[3] = hi[1];
+  }
+}
+
+__device__ __forceinline__ float fp8x1(uint32_t b) {
+  const bool special = (b & 0x7Fu) == 0x7Fu;
+  if (__builtin_expect(__ballot(special) != 0ull, 0)) return fp8_e4m3(b);
+  return __builtin_amdgcn_cvt_f32_fp8((int)b, 0);
+}
+
+// The same without a branch (byte 0 of b): the instruction, then +-480 for 0x7F / 0xFF.
+__device__ __forceinline__ float fp8x1_nb(uint32_t b) {
+  const float v = __builtin_amdgcn_cvt_f32_fp8((int)b, 0);
+  return (b & 0x7Fu) == 0x7Fu ? ((b & 0x80u) ? -480.f : 480.f) : v;
+}
+__device__ __forceinline__ void fp8x4_nb(uint32_t w, float f[4]) {
+  const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+  const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  const float v[4] = {lo[0], lo[1], hi[0], hi[1]};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t b = (w >> (8 * j)) & 0xFFu;
+    f[j] = (b & 0x7Fu) == 0x7Fu ? ((b & 0x80u) ? -480.f : 480.f) : v[j];
+  }
+}
+
+// Eight operands (two per dword, K order) for the codes of one 24/32-bit field, from a pair
+// table in LDS: entry p holds (level[p & (L-1)], level[p >> bits]) in the activation dtype,
+// one copy per lane slot, at byte (p << 8) | cb.
+template <int BITS>
+__device__ __forceinline__ u32x4 lookup8(uint32_t f, uint32_t cb, const uint32_t* tab) {
+  const char* base = reinterpret_cast<const char*>(tab);
+  u32x4 b;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t addr;
+    if constexpr (BITS == 4) {
+      addr = __builtin_amdgcn_perm(f, cb, 0x0C0C0000u | ((4u + j) << 8));  // byte j << 8 | cb
+    } else {
+      // ((f >> 6 j) & 63) << 8 | cb as one shift and one v_and_or_b32 (the compiler's own
+      // form is a shift, a mask and an add)
+      const uint32_t sh = j == 0 ? f << 8 : j == 1 ? f << 2 : j == 2 ? f >> 4 : f >> 10;
+      asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(addr) : "v"(sh), "s"(0x3F00u), "v"(cb));
+    }
+    b[j] = *reinterpret_cast<const uint32_t*>(base + addr);
+  }
+  return b;
+}
+
+// The packed words of a lane's 32-input block (four 32-bit words at 4 bits, three at 3 bits)
+// as four fields of 8 codes, transposed across the wave's rows so that field q of lane
+// (row ln, group lg) holds codes 8 lg .. 8 lg + 7 of block q of row ln: the operand the
+// 16x16x32 MFMA takes from that lane for k-slice q.
+template <int BITS, typename W>
+__device__ __forceinline__ void fields(const W& w, uint32_t r[4]) {
+  if constexpr (BITS == 4) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = w[j];
+  } else {   // the block's 96-bit stream as four 24-bit fields of 8 codes
+    r[0] = w[0];
+    r[1] = __builtin_amdgcn_alignbit(w[1], w[0], 24);
+    r[2] = __builtin_amdgcn_alignbit(w[2], w[1], 16);
+    r[3] = w[2] >> 8;
+  }
+  transpose_rows4(r);
+}
+
+// Raw buffer loads. They go through the compiler's buffer builtins, so the compiler tracks
+// each one and waits for exactly the loads a use needs. The whole byte offset goes in the
+// range-checked VGPR offset (soffset 0): an offset past the resource returns zero and fetches
+// nothing.
+template <int IMM>
+__device__ __forceinline__ void ld_x4(u32x4& d, __amdgpu_buffer_rsrc_t r, int v) {
+  d = __builtin_amdgcn_raw_buffer_load_b128(r, v + IMM, 0, 0);
+}
+template <int IMM>
+__device__ __forceinline__ void ld_x3(u32x3& d, __amdgpu_buffer_rsrc_t r, int v) {
+  d = __builtin_amdgcn_raw_buffer_load_b96(r, v + IMM, 0, 0);
+}
+template <int IMM>
+__device__ __forceinline__ void ld_x2(u32x2& d, __amdgpu_buffer_rsrc_t r, int v) {
+  d = __builtin_amdgcn_raw_buffer_load_b64(r, v + IMM, 0, 0);
+}
+template <int IMM>
+__device__ __forceinline__ void ld_x1(uint32_t& d, __amdgpu_buffer_rsrc_t r, int v) {
+  d = __builtin_amdgcn_raw_buffer_load_b32(r, v + IMM, 0, 0);
+}
+template <int IMM>
+__device__ __forceinline__ void ld_u16(uint32_t& d, __amdgpu_buffer_rsrc_t r, int v) {
+  d = __builtin_amdgcn_raw_buffer_load_b16(r, v + IMM, 0, 0);
+}
+template <int IMM>
+__device__ __forceinline__ void ld_u8(uint32_t& d, __amdgpu_buffer_rsrc_t r, int v) {
+  d = __builtin_amdgcn_raw_buffer_load_b8(r, v + IMM, 0, 0);
+}
+
+constexpr int kRsrcWord3 = 0x00020000;   // raw buffer, 32-bit data format (gfx9 family)
+constexpr int kCohere = 16;              // cache policy sc1: coherent across the device's L2s
+constexpr int kOOR = 0x7FFF0000;         // byte offset past every resource: loads return zero, fetch nothing
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
+                                           (int)(bytes > 0x7FFFFFFF ? 0x7FFFFFFF : bytes), kRsrcWord3);
+}
+
+// Host side.
+int device_cus();
+constexpr int kGemmMt = 8;   // block_m / 16 of the prefill kernels (128-slot blocks)
+// Launches the prefill kernels for a plan of 128-slot blocks (no workspace).
+int gemm_run(const char* who, bool glu, int bits, int adt, int sb, const MoeArgs& a, int64_t num_blocks,
+             hipStream_t stream);
+inline bool aligned(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
+
+}  // namespace bh

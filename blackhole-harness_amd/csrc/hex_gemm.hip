@@ -1,0 +1,305 @@
+// Fused HEX expert GEMMs for the prefill regime, on the CDNA4 matrix cores.
+//
+// Takes the place of the reference's _hex_moe_kernel (runtime/blackhole_runtime/hex_moe.py:109-151)
+// in both roles (GLU gate/up with SiLU, down with the top-k weight) when every expert gets
+// many slots. The reference sends such batches to its dequant path (hex_moe.py:357-371), which
+// writes the whole bf16 weight set and reads it back; here the packed indices go straight from
+// HBM to the matrix cores. The plan's expert blocks are 128 slots (block_m = 128).
+//
+//  * One workgroup (8 waves) per tile of 128 slots x 256 weight rows of one expert: down takes
+//    256 output rows; GLU takes 128 outputs, i.e. the same 128 rows of gate and of up. Each
+//    wave holds all 128 slots x 32 weight rows (two groups of 16; GLU: 16 gate and the same
+//    16 up rows) in 16 accumulator tiles, so every weight is decoded by exactly one wave.
+//  * The inputs run in steps of 128 (4 HEX blocks, 4 MFMA k-slices). A step's activation tile
+//    (128 gathered slot rows x 128 inputs, 32 KB) is loaded once per workgroup and staged
+//    through a two-stage LDS ring in the MFMA's fragment order, so every fragment read is one
+//    conflict-free ds_read_b128.
+//  * Each lane streams the packed words of one 32-input block per weight row group per step
+//    (128-bit loads at 4 bits), one step ahead of the math. A 4x4 transpose across the wave's
+//    rows gives each lane the 8 codes of its MFMA operand; the codes resolve through the
+//    expert's pair table in LDS (two operands per ds_read_b32, one copy per lane slot).
+//  * Order of operations, as in the decode kernels: operands are round(level); the fp32 partial
+//    of each block times its fp8 scale is added to the accumulator; the expert scale, SiLU * up
+//    and the top-k weight are applied in the epilogue in the reference's order.
+//  * Workgroups are numbered so that each XCD (its own L2) takes a contiguous run of tiles:
+//    the row tiles of a block (sharing its activation rows) and consecutive blocks of an expert
+//    (sharing its weights) run on the same L2.
+#include <string>
+#include <type_traits>
+
+#include "hex_fused.h"
+
+namespace bh {
+
+constexpr int kGThreads = 512;          // 8 waves, 32 weight rows each
+constexpr int kGWaves = kGThreads / kWave;
+constexpr int kGM = 128;                // slots of a tile: one expert block of the plan
+constexpr int kGK = 128;                // inputs per pipeline step
+constexpr int kGTile = kGM * kGK / 2;   // dwords of one step's activation tile
+constexpr int kXcds = 8;
+
+template <bool GLU>
+constexpr int gemm_cols() { return GLU ? 128 : 256; }   // outputs of a tile
+
+template <int BITS, int ADT, bool GLU, int SB>
+__global__ __launch_bounds__(kGThreads) void hex_gemm_kernel(MoeArgs a, int n_tiles) {
+  constexpr int L = 1 << BITS;
+  constexpr int NPAIR = 1 << (2 * BITS);
+  constexpr int NM = GLU ? 2 : 1;
+  constexpr int BLKB = BITS * 4;               // bytes of one 32-input block of one row
+  using W = typename std::conditional<BITS == 4, u32x4, u32x3>::type;
+  // One LDS object with the pair table first: the table sits at LDS address 0, so table reads
+  // need no base add (the 16-bit instruction offset cannot hold a base past 64 KB).
+  struct Lds {
+    uint32_t tab[NPAIR * 64];
+    uint32_t atile0[kGTile];     // the activation tile ring
+    uint32_t atile1[kGTile];
+    int slots[kGM];
+    float slot_w[GLU ? 1 : kGM];
+    uint16_t lvs[NM][L];
+  };
+  __shared__ __align__(16) Lds sm;
+  uint32_t* const tab = sm.tab;
+  uint32_t* const atile0 = sm.atile0;
+  uint32_t* const atile1 = sm.atile1;
+  int* const slots = sm.slots;
+  float* const slot_w = sm.slot_w;
+  auto& lvs = sm.lvs;
+
+  // ---- the tile: XCD x (round-robin dispatch) takes tiles [start(x), start(x) + count(x))
+  const int nwg = gridDim.x, id = blockIdx.x;
+  const int q8 = nwg / kXcds, r8 = nwg % kXcds, xcd = id % kXcds;
+  const int lin = (xcd < r8 ? xcd * (q8 + 1) : r8 * (q8 + 1) + (xcd - r8) * q8) + id / kXcds;
+  const int b = lin / n_tiles, nt = lin % n_tiles;
+  if (b >= a.npp[0] / kGM) return;
+  const int eg = a.eid[b];
+  if (eg < 0 || eg >= a.n_experts) return;
+  const int e = a.lookup[eg];
+  if (e < 0) return;
+
+  const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, lg = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nst = a.K / kGK;
+
+  // ---- stage the block's slot rows, top-k weights and levels
+  for (int r = tid; r < kGM; r += kGThreads) {
+    const int s = a.sid[(int64_t)b * kGM + r];
+    slots[r] = s;
+    if constexpr (!GLU) slot_w[r] = s < a.num_slots ? a.topk_w[s] : 0.f;
+  }
+  for (int i = tid; i < NM * L; i += kGThreads) {
+    const bh_hex_proj& w = i < L ? a.w0 : a.w1;
+    lvs[i / L][i % L] = (uint16_t)to_bits<ADT>(w.levels[(int64_t)e * L + i % L]);
+  }
+  __syncthreads();
+
+  // ---- load offsets. Activations: chunk i * 8 + wave of a step's tile is m-tile
+  // 2 i + wave / 4, k-slice wave % 4; lane (ln, lg) reads inputs 32 (wave % 4) + 8 lg .. + 7 of
+  // slot row 16 m-tile + ln.
+  const int x_rows = (int)((a.num_slots + a.a_div - 1) / a.a_div);
+  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(a.x, (int64_t)x_rows * a.s_xm * 2);
+  int xo[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int s = slots[(2 * i + (wave >> 2)) * 16 + ln];
+    xo[i] = s < a.num_slots ? (int)((int64_t)(s / a.a_div) * a.s_xm * 2) + ((wave & 3) * 32 + lg * 8) * 2 : kOOR;
+  }
+  // Weights: the wave's two groups of 16 rows; lane (ln, lg) reads block lg of the step of row
+  // ln. Down: rows 256 nt + 32 wave + 16 g. GLU: gate (g = 0) and up (g = 1) rows 128 nt + 16 wave.
+  int vw[2], vb[2];
+  uint32_t cb[2];
+  __amdgpu_buffer_rsrc_t rw[2], rb[2];
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const bh_hex_proj& w = (GLU && g == 1) ? a.w1 : a.w0;
+    rw[g] = buffer_rsrc(w.idx + (int64_t)e * w.s_ie, (int64_t)a.N * w.s_in * 4);
+    rb[g] = buffer_rsrc(w.block_scale + (int64_t)e * w.s_be, (int64_t)a.N * w.s_bn);
+    const int n = GLU ? nt * 128 + wave * 16 + ln : nt * 256 + wave * 32 + g * 16 + ln;
+    vw[g] = n < a.N ? (int)((int64_t)n * w.s_in * 4) + lg * BLKB : kOOR;
+    vb[g] = n < a.N ? (int)((int64_t)n * w.s_bn) : kOOR;
+    cb[g] = GLU ? (uint32_t)g * 128u + (lane & 31u) * 4u : lane * 4u;
+  }
+
+  // a step's activation tile, straight into LDS (buffer loads with the LDS bit): chunk
+  // i * 8 + wave, 16 bytes per lane at lane * 16. Padding rows read out of range.
+  auto load_a = [&](int st, uint32_t* at) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rx, (__attribute__((address_space(3))) void*)(at + (i * kGWaves + wave) * 256), 16,
+          xo[i] + st * (kGK * 2), 0, 0, 0);
+  };
+  auto load_w = [&](int st, W (&ws)[2], uint32_t (&sc)[2]) {
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      if constexpr (BITS == 4) ld_x4<0>(ws[g], rw[g], vw[g] + st * 4 * BLKB);
+      else ld_x3<0>(ws[g], rw[g], vw[g] + st * 4 * BLKB);
+      if constexpr (SB == 4) ld_u8<0>(sc[g], rb[g], vb[g] + st);
+      else ld_x1<0>(sc[g], rb[g], vb[g] + 4 * st);
+    }
+  };
+
+  W wa[2], wb[2];                 // weight words of the current and the next step (ping-pong)
+  uint32_t sa[2], sb[2];
+  load_w(0, wa, sa);
+  load_a(0, atile0);
+
+  // ---- the expert's pair table: entry p = (level[p & (L-1)], level[p >> bits]), 64 copies
+  // (GLU: copies 0-31 gate, 32-63 up)
+#pragma unroll
+  for (int i = 0; i < NPAIR * 16 / kGThreads; ++i) {
+    const int base = (i * kGThreads + tid) * 4;
+    const int p = base >> 6, t = GLU ? (base & 63) >> 5 : 0;
+    const uint32_t v = (uint32_t)lvs[t][p & (L - 1)] | ((uint32_t)lvs[t][p >> BITS] << 16);
+    *reinterpret_cast<u32x4*>(&tab[base]) = u32x4{v, v, v, v};
+  }
+  __builtin_amdgcn_s_waitcnt(0);         // this wave's tile chunks have landed
+  __syncthreads();
+
+  f32x4 acc[8][2];                       // [m-tile][group]
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int g = 0; g < 2; ++g) acc[j][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // One step: the next step's loads first (into the other ring stage and register set; the
+  // last step repeats its own, so every load stays unconditional), then the math of this one:
+  // the two groups' 32 operands from the table, then per m-tile j the 4 activation fragments
+  // (those of j + 1 are read before the MFMAs of j) and two interleaved 4-deep MFMA chains,
+  // whose block partials are scaled into the accumulators one m-tile later.
+  auto step = [&](int st, const uint32_t* at, uint32_t* an, const W (&cw)[2], const uint32_t (&cs)[2],
+                  W (&nw)[2], uint32_t (&ns)[2]) {
+    const int sn = st + 1 < nst ? st + 1 : st;
+    load_w(sn, nw, ns);
+    load_a(sn, an);
+    u32x4 bq[2][4];
+    float f[2][SB == 4 ? 1 : 4];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      uint32_t r[4];
+      fields<BITS>(cw[g], r);            // r[q]: block 4 st + q
+#pragma unroll
+      for (int q = 0; q < 4; ++q) bq[g][q] = lookup8<BITS>(r[q], cb[g], tab);
+      if constexpr (SB == 4) f[g][0] = fp8x1_nb(cs[g]);
+      else fp8x4_nb(cs[g], f[g]);
+    }
+    auto afrag = [&](int j, u32x4 (&av)[4]) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) av[q] = *reinterpret_cast<const u32x4*>(at + ((j * 4 + q) * 64 + lane) * 4);
+    };
+    u32x4 av[2][4];
+    f32x4 part[2][2];
+    afrag(0, av[0]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (j + 1 < 8) afrag(j + 1, av[(j + 1) & 1]);
+      const u32x4 (&x)[4] = av[j & 1];
+      if constexpr (SB == 4) {
+        f32x4 p0 = f32x4{0.f, 0.f, 0.f, 0.f}, p1 = p0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          p0 = mfma16x16x32<ADT>(x[q], bq[0][q], p0);
+          p1 = mfma16x16x32<ADT>(x[q], bq[1][q], p1);
+        }
+        part[j & 1][0] = p0;
+        part[j & 1][1] = p1;
+        if (j > 0) {
+          acc[j - 1][0] += part[(j - 1) & 1][0] * f[0][0];
+          acc[j - 1][1] += part[(j - 1) & 1][1] * f[1][0];
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 z = f32x4{0.f, 0.f, 0.f, 0.f};
+          acc[j][0] += mfma16x16x32<ADT>(x[q], bq[0][q], z) * f[0][q];
+          acc[j][1] += mfma16x16x32<ADT>(x[q], bq[1][q], z) * f[1][q];
+        }
+      }
+    }
+    if constexpr (SB == 4) {
+      acc[7][0] += part[1][0] * f[0][0];
+      acc[7][1] += part[1][1] * f[1][0];
+    }
+    __builtin_amdgcn_s_waitcnt(0);       // this wave's next-step loads have landed
+    __syncthreads();                     // every wave's chunks of the next tile; this tile is free
+  };
+  for (int st = 0; st < nst; st += 2) {
+    step(st, atile0, atile1, wa, sa, wb, sb);
+    if (st + 1 == nst) break;
+    step(st + 1, atile1, atile0, wb, sb, wa, sa);
+  }
+
+  // ---- epilogue (reference order: acc * es; silu(g) * (u * es_u); * topk weight)
+  const float es0 = a.w0.expert_scale[e], es1 = a.w1.expert_scale[e];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = j * 16 + 4 * lg + r;
+      const int slot = slots[row];
+      if (slot >= a.num_slots) continue;
+      if constexpr (GLU) {
+        const int col = nt * 128 + wave * 16 + ln;
+        if (col >= a.N) continue;
+        const float gt = acc[j][0][r] * es0;
+        const float hv = gt / (1.0f + expf(-gt)) * (acc[j][1][r] * es1);
+        reinterpret_cast<uint16_t*>(a.out)[(int64_t)slot * a.s_om + col] = (uint16_t)to_bits<ADT>(hv);
+      } else {
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          const int col = nt * 256 + wave * 32 + g * 16 + ln;
+          if (col >= a.N) continue;
+          reinterpret_cast<float*>(a.out)[(int64_t)slot * a.s_om + col] = acc[j][g][r] * es0 * slot_w[row];
+        }
+      }
+    }
+}
+
+// ----------------------------------------------------------------------------------- host side
+
+template <int BITS, int ADT, bool GLU>
+static void gemm_sb(int sb, dim3 grid, hipStream_t st, const MoeArgs& a, int n_tiles) {
+  if (sb == 1) hipLaunchKernelGGL((hex_gemm_kernel<BITS, ADT, GLU, 1>), grid, dim3(kGThreads), 0, st, a, n_tiles);
+  else hipLaunchKernelGGL((hex_gemm_kernel<BITS, ADT, GLU, 4>), grid, dim3(kGThreads), 0, st, a, n_tiles);
+}
+
+template <bool GLU>
+static void gemm_launch(int bits, int adt, int sb, dim3 grid, hipStream_t st, const MoeArgs& a, int n_tiles) {
+  if (bits == 4) {
+    if (adt == BH_HEX_BF16) gemm_sb<4, BH_HEX_BF16, GLU>(sb, grid, st, a, n_tiles);
+    else gemm_sb<4, BH_HEX_F16, GLU>(sb, grid, st, a, n_tiles);
+  } else {
+    if (adt == BH_HEX_BF16) gemm_sb<3, BH_HEX_BF16, GLU>(sb, grid, st, a, n_tiles);
+    else gemm_sb<3, BH_HEX_F16, GLU>(sb, grid, st, a, n_tiles);
+  }
+}
+
+// The 128-slot path: checks what it assumes beyond the shared checks, then launches one
+// workgroup per (block, tile of outputs). Blocks past the plan's padded length, and blocks of
+// experts outside the tier, exit at once.
+int gemm_run(const char* who, bool glu, int bits, int adt, int sb, const MoeArgs& a, int64_t num_blocks,
+             hipStream_t stream) {
+  if (a.K % kGK) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": block_m 128 needs n_in % 128 == 0");
+  if (a.K > 16384) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": block_m 128 takes n_in <= 16384");
+  const bh_hex_proj* ws[2] = {&a.w0, &a.w1};
+  for (int m = 0; m < (glu ? 2 : 1); ++m) {
+    const bh_hex_proj& w = *ws[m];
+    if ((int64_t)a.N * w.s_in * 4 > kOOR || (int64_t)a.N * w.s_bn > kOOR)
+      return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": expert matrix over 2 GiB");
+    if (sb == 1 && (w.s_bn % 4 || w.s_be % 4 || !aligned(w.block_scale, 4)))
+      return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": block_m 128 with 32-input scale blocks needs "
+                                                             "4-byte aligned block_scale rows");
+  }
+  const int64_t x_rows = cdiv(a.num_slots, a.a_div);
+  if (x_rows * a.s_xm * 2 > kOOR) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": activations over 2 GiB");
+  const int64_t n_tiles = cdiv(a.N, glu ? gemm_cols<true>() : gemm_cols<false>());
+  const int64_t wgs = num_blocks * n_tiles;
+  if (wgs > INT32_MAX) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": plan too large");
+  if (wgs == 0) return BH_HEX_OK;
+  const dim3 grid((unsigned)wgs);
+  if (glu) gemm_launch<true>(bits, adt, sb, grid, stream, a, (int)n_tiles);
+  else gemm_launch<false>(bits, adt, sb, grid, stream, a, (int)n_tiles);
+  return check_launch(who);
+}
+
+}  // namespace bh

@@ -33,67 +33,9 @@
 #include <string>
 #include <type_traits>
 
-#include "hex_common.h"
+#include "hex_fused.h"
 
 namespace bh {
-
-int check_proj(const bh_hex_proj* w, int64_t n_in, const char* who, int* block);
-
-struct MoeArgs {
-  const uint16_t* x;     // activations [rows, K] (bf16/f16 bits)
-  int64_t s_xm;
-  void* out;             // GLU: act [slots, N] (activation dtype); down: y [slots, N] float
-  int64_t s_om;
-  bh_hex_proj w0, w1;    // gate, up (GLU) or down (w0 only)
-  const int32_t* sid;
-  const int32_t* eid;
-  const int32_t* npp;
-  const int32_t* lookup;
-  const float* topk_w;
-  int64_t num_slots;
-  int32_t n_experts;
-  int32_t a_div;
-  int32_t N, K;
-  int32_t scale_words;   // block_scale rows allow one load of a unit's scales (8 or 2 bytes)
-                         // (host only: it selects the whole-unit kernel variant)
-  float* part;           // workspace: partial sums of items split between workgroups
-  int32_t* counters;     // workspace: arrivals per split item (64 bytes apart), zero between calls
-};
-
-// Four fp8 scales (one byte each) -> float, by the conversion instruction; a wave holding a
-// 0x7F / 0xFF code (NaN for the instruction, +-480 for the reference formula) takes the formula.
-__device__ __forceinline__ void fp8x4(uint32_t w, float f[4]) {
-  const bool special = (((w & 0x7F7F7F7Fu) + 0x01010101u) & 0x80808080u) != 0u;
-  if (__builtin_expect(__ballot(special) != 0ull, 0)) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) f[j] = fp8_e4m3((w >> (8 * j)) & 0xFFu);
-  } else {
-    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
-    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
-    f[0] = lo[0]; f[1] = lo[1]; f[2] = hi[0]; f[3] = hi[1];
-  }
-}
-
-__device__ __forceinline__ float fp8x1(uint32_t b) {
-  const bool special = (b & 0x7Fu) == 0x7Fu;
-  if (__builtin_expect(__ballot(special) != 0ull, 0)) return fp8_e4m3(b);
-  return __builtin_amdgcn_cvt_f32_fp8((int)b, 0);
-}
-
-// Eight operands (two per dword, K order) for the codes of one 24/32-bit field.
-template <int BITS>
-__device__ __forceinline__ u32x4 lookup8(uint32_t f, uint32_t cb, const uint32_t* tab) {
-  const char* base = reinterpret_cast<const char*>(tab);
-  u32x4 b;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    uint32_t addr;
-    if constexpr (BITS == 4) addr = __builtin_amdgcn_perm(f, cb, 0x0C0C0000u | ((4u + j) << 8));  // byte j << 8 | cb
-    else addr = (((f >> (6 * j)) & 63u) << 8) | cb;
-    b[j] = *reinterpret_cast<const uint32_t*>(base + addr);
-  }
-  return b;
-}
 
 // One unit's loads of one wave: two 128-input steps.
 template <int BITS, int NM, int SB, bool KF>
@@ -116,41 +58,8 @@ struct ItemRes {
   int vw[NM], vb[NM];              // lane offsets: row n, block lane / 16 of the unit
 };
 
-// Buffer loads of the hot loop. They go through the compiler's buffer builtins, so the
-// compiler tracks each one and waits for exactly the loads a use needs; the loop keeps every
-// load unconditional and in a fixed order, so those waits stay partial (vmcnt(N), not 0).
-template <int IMM>
-__device__ __forceinline__ void ld_x4(u32x4& d, __amdgpu_buffer_rsrc_t r, int v) {
-  d = __builtin_amdgcn_raw_buffer_load_b128(r, v + IMM, 0, 0);
-}
-template <int IMM>
-__device__ __forceinline__ void ld_x3(u32x3& d, __amdgpu_buffer_rsrc_t r, int v) {
-  d = __builtin_amdgcn_raw_buffer_load_b96(r, v + IMM, 0, 0);
-}
-template <int IMM>
-__device__ __forceinline__ void ld_x2(u32x2& d, __amdgpu_buffer_rsrc_t r, int v) {
-  d = __builtin_amdgcn_raw_buffer_load_b64(r, v + IMM, 0, 0);
-}
-template <int IMM>
-__device__ __forceinline__ void ld_x1(uint32_t& d, __amdgpu_buffer_rsrc_t r, int v) {
-  d = __builtin_amdgcn_raw_buffer_load_b32(r, v + IMM, 0, 0);
-}
-template <int IMM>
-__device__ __forceinline__ void ld_u16(uint32_t& d, __amdgpu_buffer_rsrc_t r, int v) {
-  d = __builtin_amdgcn_raw_buffer_load_b16(r, v + IMM, 0, 0);
-}
-template <int IMM>
-__device__ __forceinline__ void ld_u8(uint32_t& d, __amdgpu_buffer_rsrc_t r, int v) {
-  d = __builtin_amdgcn_raw_buffer_load_b8(r, v + IMM, 0, 0);
-}
-
-constexpr int kRsrcWord3 = 0x00020000;   // raw buffer, 32-bit data format (gfx9 family)
-constexpr int kCohere = 16;              // cache policy sc1: coherent across the device's L2s
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int64_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
-                                           (int)(bytes > 0x7FFFFFFF ? 0x7FFFFFFF : bytes), kRsrcWord3);
-}
+// The hot loop keeps every load unconditional and in a fixed order, so the compiler's waits
+// for them stay partial (vmcnt(N), not 0).
 
 // Expert blocks a workgroup's unit range may touch (their experts and slot rows are staged in
 // LDS); the launch sizes the grid so no range needs more. At 16-slot blocks; 64 / MT in general.
@@ -167,8 +76,6 @@ constexpr int kMinUnits = 2;             // units per workgroup below which the 
 // per trip publishes them.
 template <int MT, bool GLU>
 constexpr int trip() { return GLU ? (MT == 1 ? 2 : 1) : (MT == 4 ? 1 : 2); }
-
-constexpr int kOOR = 0x7FFF0000;   // byte offset past every resource: loads return zero, fetch nothing
 
 // Position of a unit: block (relative to the range's first), row tile, unit within the item.
 struct Pos {
@@ -368,18 +275,7 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int m = 0; m < NM; ++m) {
-        if constexpr (BITS == 4) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) r[h][m][j] = st.w[m][h][j];
-        } else {   // the block's 96-bit stream as four 24-bit fields of 8 codes
-          r[h][m][0] = st.w[m][h][0];
-          r[h][m][1] = __builtin_amdgcn_alignbit(st.w[m][h][1], st.w[m][h][0], 24);
-          r[h][m][2] = __builtin_amdgcn_alignbit(st.w[m][h][2], st.w[m][h][1], 16);
-          r[h][m][3] = st.w[m][h][2] >> 8;
-        }
-        transpose_rows4(r[h][m]);  // r[h][m][q] = field lg of block 8 s + 4 h + q
-      }
+      for (int m = 0; m < NM; ++m) fields<BITS>(st.w[m][h], r[h][m]);   // r[h][m][q]: block 8 s + 4 h + q
     const int nk = KF ? 8 : min(8, nb32 - 8 * s);   // valid k-slices of this unit
     u32x4 bq[2][NM], av[2][MT];
     auto fetch = [&](int k, int slot) {
@@ -728,9 +624,7 @@ static void launch_moe(int bits, int adt, int mt, int sb, dim3 grid, hipStream_t
   }
 }
 
-static bool aligned(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
-
-static int device_cus() {
+int device_cus() {
   static int cus[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
@@ -775,8 +669,8 @@ static int check_moe(const char* who, int32_t bits, int32_t adt, int64_t n_out, 
   if (adt != BH_HEX_BF16 && adt != BH_HEX_F16)
     return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": activations must be BF16 or F16");
   if (!tile) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": null tile");
-  if (tile->block_m != 16 && tile->block_m != 32 && tile->block_m != 64)
-    return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": block_m must be 16, 32 or 64");
+  if (tile->block_m != 16 && tile->block_m != 32 && tile->block_m != 64 && tile->block_m != 128)
+    return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": block_m must be 16, 32, 64 or 128");
   if (tile->block_n != kRows || tile->k_split != 1)
     return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": block_n must be 256 and k_split 1");
   if (n_out <= 0 || n_out > (1 << 30) || n_in > (1 << 30)) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": bad width");
@@ -852,9 +746,6 @@ extern "C" int bh_hex_moe_glu(const void* x, int32_t x_dtype, int64_t s_xm, void
   if (s_xm % 8 || !aligned(x, 16)) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": x rows must be 16-byte aligned");
   if (cdiv(num_slots, a_div) * s_xm * 2 > 0x7FFFFFFF) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": x over 2 GiB");
   if (num_blocks == 0 || num_slots == 0) return BH_HEX_OK;
-  dim3 grid;
-  if ((rc = attach_workspace(who, counters, n_counters, partials, n_partials, num_blocks, n_out, n_in, mt, true, a,
-                             &grid))) return rc;
   a.x = reinterpret_cast<const uint16_t*>(x);
   a.s_xm = s_xm;
   a.out = act;
@@ -863,6 +754,10 @@ extern "C" int bh_hex_moe_glu(const void* x, int32_t x_dtype, int64_t s_xm, void
   a.w1 = *up;
   a.a_div = a_div;
   a.scale_words = words;
+  if (mt == kGemmMt) return gemm_run(who, true, bits, x_dtype, sb, a, num_blocks, reinterpret_cast<hipStream_t>(stream));
+  dim3 grid;
+  if ((rc = attach_workspace(who, counters, n_counters, partials, n_partials, num_blocks, n_out, n_in, mt, true, a,
+                             &grid))) return rc;
   launch_moe<true>(bits, x_dtype, mt, sb, grid, reinterpret_cast<hipStream_t>(stream), a);
   return check_launch(who);
 }
@@ -884,9 +779,6 @@ extern "C" int bh_hex_moe_down(const void* act, int32_t act_dtype, int64_t s_am,
   if (s_am % 8 || !aligned(act, 16)) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": act rows must be 16-byte aligned");
   if (num_slots * s_am * 2 > 0x7FFFFFFF) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": act over 2 GiB");
   if (num_blocks == 0 || num_slots == 0) return BH_HEX_OK;
-  dim3 grid;
-  if ((rc = attach_workspace(who, counters, n_counters, partials, n_partials, num_blocks, n_out, n_in, mt, false, a,
-                             &grid))) return rc;
   a.x = reinterpret_cast<const uint16_t*>(act);
   a.s_xm = s_am;
   a.out = y;
@@ -896,6 +788,10 @@ extern "C" int bh_hex_moe_down(const void* act, int32_t act_dtype, int64_t s_am,
   a.topk_w = topk_w;
   a.a_div = 1;
   a.scale_words = words;
+  if (mt == kGemmMt) return gemm_run(who, false, bits, act_dtype, sb, a, num_blocks, reinterpret_cast<hipStream_t>(stream));
+  dim3 grid;
+  if ((rc = attach_workspace(who, counters, n_counters, partials, n_partials, num_blocks, n_out, n_in, mt, false, a,
+                             &grid))) return rc;
   launch_moe<false>(bits, act_dtype, mt, sb, grid, reinterpret_cast<hipStream_t>(stream), a);
   return check_launch(who);
 }
@@ -904,8 +800,13 @@ extern "C" int bh_hex_moe_workspace(int64_t num_blocks, int64_t n_out, int64_t n
                                     int64_t* n_counters, int64_t* n_partials) {
   if (num_blocks < 0 || n_out <= 0 || n_in <= 0 || !n_counters || !n_partials)
     return fail(BH_HEX_ERR_VALUE, "bh_hex_moe_workspace: bad arguments");
-  if (block_m != 16 && block_m != 32 && block_m != 64)
-    return fail(BH_HEX_ERR_UNSUPPORTED, "bh_hex_moe_workspace: block_m must be 16, 32 or 64");
+  if (block_m != 16 && block_m != 32 && block_m != 64 && block_m != 128)
+    return fail(BH_HEX_ERR_UNSUPPORTED, "bh_hex_moe_workspace: block_m must be 16, 32, 64 or 128");
+  if (block_m / 16 == kGemmMt) {     // the 128-slot kernels need no workspace
+    *n_counters = 0;
+    *n_partials = 0;
+    return BH_HEX_OK;
+  }
   const Workspace w = workspace_layout(num_blocks, n_out, n_in, block_m / 16, glu != 0);
   *n_counters = w.counters;
   *n_partials = w.partials;

@@ -58,6 +58,7 @@ def test_workspace_sizes():
     assert rc == _lib.OK and nc == 104 * 3 * 16 and npart > 0
     rc, nc2, npart2 = _workspace(lib, 104, 768, 2048, 64, 1)
     assert nc2 == nc and npart2 > npart          # partial tiles grow with block_m
+    assert _workspace(lib, 104, 768, 2048, 128, 1) == (_lib.OK, 0, 0)   # the prefill kernels need none
 
 
 def _status(rc, code, pattern):
@@ -96,6 +97,11 @@ def test_host_side_errors():
     _status(lib.bh_hex_moe_glu(16, _lib.BF16, 64, 16, 64, ctypes.byref(w32), ctypes.byref(w32), 4, 64, 64,
                                16, 16, 1, 16, 16, 4, 4, 1, ctypes.byref(tile), None, 0, None, 0, None),
             _lib.ERR_VALUE, "workspace")
+    # the 128-slot kernels step through the inputs 128 at a time
+    _status(lib.bh_hex_moe_glu(16, _lib.BF16, 64, 16, 64, ctypes.byref(w32), ctypes.byref(w32), 4, 64, 64,
+                               16, 16, 1, 16, 16, 4, 4, 1, ctypes.byref(_lib.HexTile(128, 256, 1)), None, 0, None, 0,
+                               None),
+            _lib.ERR_UNSUPPORTED, r"n_in % 128")
     _status(lib.bh_hex_moe_reduce(16, 6, 16, _lib.I64, 4, 2, 2, 6, 16, _lib.BF16, 6, None),
             _lib.ERR_UNSUPPORTED, "H % 4")
 

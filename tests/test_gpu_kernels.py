@@ -191,7 +191,7 @@ def test_reference_suite_shapes(T, split, bits):
     assert run_fused(ref, tiers, T, E, k, H, dt=torch.float32, seed=T, path="auto") < 1e-4
 
 
-@pytest.mark.parametrize("bm", [16, 32, 64])
+@pytest.mark.parametrize("bm", [16, 32, 64, 128])
 @pytest.mark.parametrize("block", [32, 128])
 def test_tiles(bm, block):
     say(f"tiles bm={bm} block={block}")
@@ -213,6 +213,22 @@ def test_items_split_between_workgroups(T):
     ref, tiers = make_layer(E, H, I, 0, (4,), seed=11, block=128)
     for _ in range(2):
         assert run_fused(ref, tiers, T, E, k, H, seed=T) < TOL_16
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("block", [32, 128])
+def test_prefill_kernels(dt, block):
+    """The 128-slot prefill kernels at batches where each expert fills several blocks (plus a
+    partly filled one): two tiers (4 and 3 bits), down outputs (384) not a multiple of the
+    256-row tile, Zipf-skewed routing; twice in a row."""
+    say(f"prefill kernels {dt} block={block}")
+    E, H, I, k = 8, 384, 256, 2
+    ref, tiers = make_layer(E, H, I, 3, (4, 3), seed=31, block=block)
+    for T, skew in ((600, False), (700, True), (600, False)):
+        err = run_fused(ref, tiers, T, E, k, H, dt=dt, seed=T, config={"BLOCK_M": 128}, skew=skew)
+        assert err < TOL_16, (T, err)
+    # and chosen by default at that batch (more than 64 slots per expert)
+    assert hm.default_config(1200, I, H, True, E)["BLOCK_M"] == 128
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
@@ -281,7 +297,7 @@ def test_down_kernel_exact(bits):
     Wd = O.dequant(parts["down_proj"]["idx"], parts["down_proj"]["block_scale"], parts["down_proj"]["expert_scale"],
                    parts["down_proj"]["levels"], bits, "R").astype(np.float64)
     want = np.stack([Wd[ids.reshape(-1)[s]] @ act[s].astype(np.float64) * 0.5 for s in range(S)])
-    for bm in (16, 32, 64):
+    for bm in (16, 32, 64, 128):
         sid, eid, npp = hm.plan(torch.from_numpy(ids).to(DEV).reshape(-1), E, bm, "torch")
         y = torch.full((S, H), float("nan"), device=DEV)
         hm._launch_down(torch.from_numpy(act).to(torch.bfloat16).to(DEV), y, tier, sid, eid, npp, S,
@@ -310,27 +326,29 @@ def test_width_mismatch_and_dtype_errors():
         hm.hex_moe_fused(torch.zeros(2, H, device=DEV), w, ids, tiers)
 
 
-def test_graph_capture_replays_match_eager():
+@pytest.mark.parametrize("bm", [None, 128])
+def test_graph_capture_replays_match_eager(bm):
     """The fused path captured in a hipGraph: several replays, with eager work between them,
-    each equal to the eager result."""
-    say("graph capture")
-    E, H, I, k, T = 16, 256, 128, 4, 8
+    each equal to the eager result (default tiles, and the 128-slot prefill kernels)."""
+    say(f"graph capture bm={bm}")
+    E, H, I, k, T = 16, 256, 128, 4, 8 if bm is None else 300
+    cfg = None if bm is None else {"BLOCK_M": bm}
     ref, tiers = make_layer(E, H, I, 8, (4, 3), seed=12)
     w, ids = routing(T, E, k, seed=5)
     x = torch.randn(T, H, generator=torch.Generator().manual_seed(0)).to(torch.bfloat16).to(DEV)
     wd, idd = torch.from_numpy(w).to(DEV), torch.from_numpy(ids).to(DEV)
-    eager = hm.hex_moe_fused(x, wd, idd, tiers)
+    eager = hm.hex_moe_fused(x, wd, idd, tiers, cfg)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        hm.hex_moe_fused(x, wd, idd, tiers)
+        hm.hex_moe_fused(x, wd, idd, tiers, cfg)
     torch.cuda.current_stream().wait_stream(s)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        out = hm.hex_moe_fused(x, wd, idd, tiers)
+        out = hm.hex_moe_fused(x, wd, idd, tiers, cfg)
     for i in range(3):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager), i
-        _ = hm.hex_moe_fused(x * 2, wd, idd, tiers)      # unrelated eager work between replays
+        _ = hm.hex_moe_fused(x * 2, wd, idd, tiers, cfg)      # unrelated eager work between replays
         torch.cuda.synchronize()

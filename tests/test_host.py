@@ -54,14 +54,18 @@ def test_block_from_shapes_128():
 def test_default_config_and_env(monkeypatch):
     assert hm.default_config(8, 768, 2048, True, 96) == {"BLOCK_M": 16, "BLOCK_N": 256}    # T=1 decode
     assert hm.default_config(128, 768, 2048, True, 96)["BLOCK_M"] == 16                    # T=16
-    assert hm.default_config(32768, 2048, 768, False, 96)["BLOCK_M"] == 64                 # prefill
+    assert hm.default_config(32768, 2048, 768, False, 96)["BLOCK_M"] == 128                # prefill
+    assert hm.default_config(32768, 2048, 96, False, 96)["BLOCK_M"] == 64                  # inputs % 128 != 0
     assert hm.default_config(3000, 768, 2048, True, 96)["BLOCK_M"] == 32
+    assert hm.default_config(6000, 768, 2048, True, 96)["BLOCK_M"] == 64
     monkeypatch.setenv("BLACKHOLE_HEX_TILES", "64")
     assert hm.default_config(8, 768, 2048, True, 96) == {"BLOCK_M": 64, "BLOCK_N": 256}
     # the reference's own config keys map onto the tile
     assert hm._tile_from({"BLOCK_M": 16, "BLOCK_N": 32, "BLOCK_K": 32, "num_warps": 4, "num_stages": 1}) == 16
-    assert hm._tile_from({"BLOCK_M": 128, "BLOCK_N": 128}) == 64
+    assert hm._tile_from({"BLOCK_M": 64, "BLOCK_N": 128}) == 64
+    assert hm._tile_from({"BLOCK_M": 128, "BLOCK_N": 128}) == 128
     assert hm._tile_from({"BLOCK_M": 24}) == 32
+    assert hm._fit_tile(128, 768) == 128 and hm._fit_tile(128, 160) == 64 and hm._fit_tile(32, 160) == 32
 
 
 def test_kernels_refuse_cpu_tensors():
