@@ -172,10 +172,11 @@ def _tile_from(cfg: dict) -> int:
     return 16 if bm <= 16 else (32 if bm <= 32 else (64 if bm <= 64 else 128))
 
 
-def _fit_tile(bm: int, n_in: int) -> int:
-    """The prefill kernels (block_m 128) step through the inputs 128 at a time; other widths
-    take the 64-slot decode kernels."""
-    return 64 if bm == 128 and n_in % 128 else bm
+def _fit_tile(bm: int, n_in: int, n_out: int, glu: bool) -> int:
+    """The prefill kernels (block_m 128) step through the inputs 128 at a time and write output
+    rows (act in the activation dtype, y in float32) 16 bytes at a time; other widths take the
+    64-slot decode kernels."""
+    return 64 if bm == 128 and (n_in % 128 or n_out % (8 if glu else 4)) else bm
 
 
 def default_config(slots: int, n_out: int, n_in: int, glu: bool, n_experts: int = 0) -> dict:
@@ -187,7 +188,7 @@ def default_config(slots: int, n_out: int, n_in: int, glu: bool, n_experts: int 
     else:
         per_expert = slots / max(1, n_experts or slots)
         bm = 16 if per_expert <= 16 else (32 if per_expert <= 48 else (64 if per_expert <= PREFILL_MIN else 128))
-    return {"BLOCK_M": _fit_tile(bm, n_in), "BLOCK_N": 256}
+    return {"BLOCK_M": _fit_tile(bm, n_in, n_out, glu), "BLOCK_N": 256}
 
 
 # --------------------------------------------------------------------------- fused path
@@ -281,8 +282,8 @@ def hex_moe_fused(x, topk_weights, topk_ids, tiers: list[HexTier], config: dict 
     y = (torch.empty if _covers_all(tiers) else torch.zeros)(S, H, dtype=torch.float32, device=x.device)
     c1 = config or default_config(S, I, H, True, E)
     c2 = config or default_config(S, H, I, False, E)
-    bm1 = _fit_tile(_tile_from(c1), H)
-    bm2 = _fit_tile(_tile_from(c2), I)
+    bm1 = _fit_tile(_tile_from(c1), H, I, True)
+    bm2 = _fit_tile(_tile_from(c2), I, H, False)
     p1 = plan(flat, E, bm1, align_mode)
     p2 = p1 if bm2 == bm1 else plan(flat, E, bm2, align_mode)
     for t in tiers:

@@ -38,6 +38,12 @@ constexpr int kGK = 128;                // inputs per pipeline step
 constexpr int kGTile = kGM * kGK / 2;   // dwords of one step's activation tile
 constexpr int kXcds = 8;
 
+constexpr int kTileLoads = 4;           // buffer loads per lane of one step's activation tile
+
+// s_waitcnt operand that waits until at most n vector-memory loads are in flight (gfx9:
+// vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima)
+constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
 template <bool GLU>
 constexpr int gemm_cols() { return GLU ? 128 : 256; }   // outputs of a tile
 
@@ -48,30 +54,34 @@ __global__ __launch_bounds__(kGThreads) void hex_gemm_kernel(MoeArgs a, int n_ti
   constexpr int NM = GLU ? 2 : 1;
   constexpr int BLKB = BITS * 4;               // bytes of one 32-input block of one row
   using W = typename std::conditional<BITS == 4, u32x4, u32x3>::type;
+  // Activation ring depth: tiles are loaded one step ahead of the math, as are the weight
+  // words (two register sets). (Two steps ahead measured no faster.)
+  constexpr int D = 2;
   // One LDS object with the pair table first: the table sits at LDS address 0, so table reads
   // need no base add (the 16-bit instruction offset cannot hold a base past 64 KB).
   struct Lds {
     uint32_t tab[NPAIR * 64];
-    uint32_t atile0[kGTile];     // the activation tile ring
-    uint32_t atile1[kGTile];
+    uint32_t atile[D][kGTile];   // the activation tile ring
     int slots[kGM];
     float slot_w[GLU ? 1 : kGM];
     uint16_t lvs[NM][L];
   };
   __shared__ __align__(16) Lds sm;
   uint32_t* const tab = sm.tab;
-  uint32_t* const atile0 = sm.atile0;
-  uint32_t* const atile1 = sm.atile1;
   int* const slots = sm.slots;
   float* const slot_w = sm.slot_w;
   auto& lvs = sm.lvs;
 
-  // ---- the tile: XCD x (round-robin dispatch) takes tiles [start(x), start(x) + count(x))
-  const int nwg = gridDim.x, id = blockIdx.x;
-  const int q8 = nwg / kXcds, r8 = nwg % kXcds, xcd = id % kXcds;
-  const int lin = (xcd < r8 ? xcd * (q8 + 1) : r8 * (q8 + 1) + (xcd - r8) * q8) + id / kXcds;
+  // ---- the tile. Workgroup id runs on XCD id % 8 (round-robin dispatch). The tiles in use
+  // (blocks within the padded length, known only here) are split evenly over the XCDs, each
+  // XCD taking a contiguous run; XCD x holds at least as many workgroups as its share, and the
+  // rest exit.
+  const int used = (a.npp[0] / kGM) * n_tiles;
+  const int xcd = blockIdx.x % kXcds, loc = blockIdx.x / kXcds;
+  const int q8 = used / kXcds, r8 = used % kXcds;
+  if (loc >= q8 + (xcd < r8 ? 1 : 0)) return;
+  const int lin = (xcd < r8 ? xcd * (q8 + 1) : r8 * (q8 + 1) + (xcd - r8) * q8) + loc;
   const int b = lin / n_tiles, nt = lin % n_tiles;
-  if (b >= a.npp[0] / kGM) return;
   const int eg = a.eid[b];
   if (eg < 0 || eg >= a.n_experts) return;
   const int e = a.lookup[eg];
@@ -122,27 +132,30 @@ __global__ __launch_bounds__(kGThreads) void hex_gemm_kernel(MoeArgs a, int n_ti
 
   // a step's activation tile, straight into LDS (buffer loads with the LDS bit): chunk
   // i * 8 + wave, 16 bytes per lane at lane * 16. Padding rows read out of range.
+  auto load_a1 = [&](int st, int i, uint32_t* at) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)(at + (i * kGWaves + wave) * 256),
+                                             16, xo[i] + st * (kGK * 2), 0, 0, 0);
+  };
   auto load_a = [&](int st, uint32_t* at) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rx, (__attribute__((address_space(3))) void*)(at + (i * kGWaves + wave) * 256), 16,
-          xo[i] + st * (kGK * 2), 0, 0, 0);
+    for (int i = 0; i < 4; ++i) load_a1(st, i, at);
+  };
+  auto load_w1 = [&](int st, int g, W& w, uint32_t& sc) {
+    if constexpr (BITS == 4) ld_x4<0>(w, rw[g], vw[g] + st * 4 * BLKB);
+    else ld_x3<0>(w, rw[g], vw[g] + st * 4 * BLKB);
+    if constexpr (SB == 4) ld_u8<0>(sc, rb[g], vb[g] + st);
+    else ld_x1<0>(sc, rb[g], vb[g] + 4 * st);
   };
   auto load_w = [&](int st, W (&ws)[2], uint32_t (&sc)[2]) {
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      if constexpr (BITS == 4) ld_x4<0>(ws[g], rw[g], vw[g] + st * 4 * BLKB);
-      else ld_x3<0>(ws[g], rw[g], vw[g] + st * 4 * BLKB);
-      if constexpr (SB == 4) ld_u8<0>(sc[g], rb[g], vb[g] + st);
-      else ld_x1<0>(sc[g], rb[g], vb[g] + 4 * st);
-    }
+    for (int g = 0; g < 2; ++g) load_w1(st, g, ws[g], sc[g]);
   };
 
-  W wa[2], wb[2];                 // weight words of the current and the next step (ping-pong)
-  uint32_t sa[2], sb[2];
-  load_w(0, wa, sa);
-  load_a(0, atile0);
+  W ws[2][2];                     // weight words of this step and the next (ping-pong)
+  uint32_t ss[2][2];
+  load_w(0, ws[0], ss[0]);
+#pragma unroll
+  for (int d = 0; d < D - 1; ++d) load_a(d < nst ? d : nst - 1, sm.atile[d]);
 
   // ---- the expert's pair table: entry p = (level[p & (L-1)], level[p >> bits]), 64 copies
   // (GLU: copies 0-31 gate, 32-63 up)
@@ -153,7 +166,7 @@ __global__ __launch_bounds__(kGThreads) void hex_gemm_kernel(MoeArgs a, int n_ti
     const uint32_t v = (uint32_t)lvs[t][p & (L - 1)] | ((uint32_t)lvs[t][p >> BITS] << 16);
     *reinterpret_cast<u32x4*>(&tab[base]) = u32x4{v, v, v, v};
   }
-  __builtin_amdgcn_s_waitcnt(0);         // this wave's tile chunks have landed
+  __builtin_amdgcn_s_waitcnt(vm_wait(kTileLoads * (D - 2)));   // step 0's loads have landed
   __syncthreads();
 
   f32x4 acc[8][2];                       // [m-tile][group]
@@ -162,16 +175,24 @@ __global__ __launch_bounds__(kGThreads) void hex_gemm_kernel(MoeArgs a, int n_ti
 #pragma unroll
     for (int g = 0; g < 2; ++g) acc[j][g] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // One step: the next step's loads first (into the other ring stage and register set; the
-  // last step repeats its own, so every load stays unconditional), then the math of this one:
+  // One step (phase P = st % D): the loads of step st + D - 1 first (into the ring stage and
+  // register set that step st - 1 used; past the end the last step repeats, so every load
+  // stays unconditional), then the math of this one:
   // the two groups' 32 operands from the table, then per m-tile j the 4 activation fragments
   // (those of j + 1 are read before the MFMAs of j) and two interleaved 4-deep MFMA chains,
   // whose block partials are scaled into the accumulators one m-tile later.
-  auto step = [&](int st, const uint32_t* at, uint32_t* an, const W (&cw)[2], const uint32_t (&cs)[2],
-                  W (&nw)[2], uint32_t (&ns)[2]) {
-    const int sn = st + 1 < nst ? st + 1 : st;
-    load_w(sn, nw, ns);
-    load_a(sn, an);
+  auto step = [&](int st, auto phase) {
+    constexpr int P = decltype(phase)::value;
+    const uint32_t* at = sm.atile[st % D];
+    const W (&cw)[2] = ws[P];
+    const uint32_t (&cs)[2] = ss[P];
+    const int sw = st + 1 < nst ? st + 1 : st;
+    const int sa = st + D - 1 < nst ? st + D - 1 : nst - 1;
+    uint32_t* const an = sm.atile[(st + D - 1) % D];
+    // (scheduling barriers keep each phase's LDS reads ahead of the MFMAs that use them, and
+    // the next step's loads spread over the m-tiles: issued back to back at the start of a
+    // step, 64 loads per compute unit hold every wave at the memory pipe before its MFMAs)
+    __builtin_amdgcn_sched_barrier(0);
     u32x4 bq[2][4];
     float f[2][SB == 4 ? 1 : 4];
 #pragma unroll
@@ -192,7 +213,11 @@ __global__ __launch_bounds__(kGThreads) void hex_gemm_kernel(MoeArgs a, int n_ti
     afrag(0, av[0]);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
+      __builtin_amdgcn_sched_barrier(0);
       if (j + 1 < 8) afrag(j + 1, av[(j + 1) & 1]);
+      if (j < 2) load_w1(sw, j, ws[1 - P][j], ss[1 - P][j]);
+      else if (j < 6) load_a1(sa, j - 2, an);
+      __builtin_amdgcn_sched_barrier(0);
       const u32x4 (&x)[4] = av[j & 1];
       if constexpr (SB == 4) {
         f32x4 p0 = f32x4{0.f, 0.f, 0.f, 0.f}, p1 = p0;
@@ -220,39 +245,85 @@ __global__ __launch_bounds__(kGThreads) void hex_gemm_kernel(MoeArgs a, int n_ti
       acc[7][0] += part[1][0] * f[0][0];
       acc[7][1] += part[1][1] * f[1][0];
     }
-    __builtin_amdgcn_s_waitcnt(0);       // this wave's next-step loads have landed
+    // step st + 1's words and tile have landed (the tile loads issued after its words, for
+    // D - 2 steps further on, stay in flight)
+    __builtin_amdgcn_s_waitcnt(vm_wait(kTileLoads * (D - 2)));
     __syncthreads();                     // every wave's chunks of the next tile; this tile is free
   };
-  for (int st = 0; st < nst; st += 2) {
-    step(st, atile0, atile1, wa, sa, wb, sb);
-    if (st + 1 == nst) break;
-    step(st + 1, atile1, atile0, wb, sb, wa, sa);
+  // pairs of steps (the register set of a step is a compile-time constant), then the last one
+  int st = 0;
+  for (; st + 2 <= nst; st += 2) {
+    step(st, std::integral_constant<int, 0>());
+    step(st + 1, std::integral_constant<int, 1>());
   }
+  if (st < nst) step(st, std::integral_constant<int, 0>());
 
-  // ---- epilogue (reference order: acc * es; silu(g) * (u * es_u); * topk weight)
+  // ---- epilogue (reference order: acc * es; silu(g) * (u * es_u); * topk weight). The
+  // outputs go through the (now free) activation ring so that each slot row is written with
+  // 16-byte stores: GLU's 128 x 128 tile at once (rows of 136 halves), down's 128 x 256 floats
+  // in two halves of 64 slots (rows of 260 floats); the padding staggers the banks.
   const float es0 = a.w0.expert_scale[e], es1 = a.w1.expert_scale[e];
+  uint32_t* const stage = sm.atile[0];                   // stages 0 and 1: 64 KB in a row
+  if constexpr (GLU) {
+    constexpr int RS = 136;                              // halves per staged row
+    uint16_t* const st16 = reinterpret_cast<uint16_t*>(stage);
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
+    for (int j = 0; j < 8; ++j)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = j * 16 + 4 * lg + r;
-      const int slot = slots[row];
-      if (slot >= a.num_slots) continue;
-      if constexpr (GLU) {
-        const int col = nt * 128 + wave * 16 + ln;
-        if (col >= a.N) continue;
+      for (int r = 0; r < 4; ++r) {
         const float gt = acc[j][0][r] * es0;
-        const float hv = gt / (1.0f + expf(-gt)) * (acc[j][1][r] * es1);
-        reinterpret_cast<uint16_t*>(a.out)[(int64_t)slot * a.s_om + col] = (uint16_t)to_bits<ADT>(hv);
-      } else {
+        const float hv = gt * __builtin_amdgcn_rcpf(1.0f + __expf(-gt)) * (acc[j][1][r] * es1);
+        st16[(j * 16 + 4 * lg + r) * RS + wave * 16 + ln] = (uint16_t)to_bits<ADT>(hv);
+      }
+    __syncthreads();
+    // 16 threads per row, 8 outputs (16 bytes) each
 #pragma unroll
-        for (int g = 0; g < 2; ++g) {
-          const int col = nt * 256 + wave * 32 + g * 16 + ln;
-          if (col >= a.N) continue;
-          reinterpret_cast<float*>(a.out)[(int64_t)slot * a.s_om + col] = acc[j][g][r] * es0 * slot_w[row];
+    for (int it = 0; it < kGM * 16 / kGThreads; ++it) {
+      const int row = it * (kGThreads / 16) + tid / 16, c = (tid & 15) * 8;
+      const int slot = slots[row], col = nt * 128 + c;
+      if (slot >= a.num_slots || col >= a.N) continue;
+      uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + (int64_t)slot * a.s_om + col;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(st16 + row * RS + c);
+      if (col + 8 <= a.N) {
+        *reinterpret_cast<u32x4*>(dst) = v;
+      } else {
+        for (int q = 0; q < a.N - col; ++q) dst[q] = st16[row * RS + c + q];
+      }
+    }
+  } else {
+    // 64 rows of 256 floats fill the 64 KB exactly: instead of padding, column bits 4-5 are
+    // XORed with row bits 2-3 (conflict-free writes; 4-float chunks stay contiguous)
+    float* const stf = reinterpret_cast<float*>(stage);
+    auto at_rc = [](int row, int col) { return row * 256 + (col ^ (((row >> 2) & 3) << 4)); };
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if (h) __syncthreads();                            // the first half's readers are done
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = j * 16 + 4 * lg + r;           // within the half
+          const float w = slot_w[h * 64 + row];
+#pragma unroll
+          for (int g = 0; g < 2; ++g) stf[at_rc(row, wave * 32 + g * 16 + ln)] = acc[h * 4 + j][g][r] * es0 * w;
+        }
+      __syncthreads();
+      // 64 threads per row, 4 outputs (16 bytes) each
+#pragma unroll
+      for (int it = 0; it < 64 * 64 / kGThreads; ++it) {
+        const int row = it * (kGThreads / 64) + tid / 64, c = (tid & 63) * 4;
+        const int slot = slots[h * 64 + row], col = nt * 256 + c;
+        if (slot >= a.num_slots || col >= a.N) continue;
+        float* dst = reinterpret_cast<float*>(a.out) + (int64_t)slot * a.s_om + col;
+        const f32x4 v = *reinterpret_cast<const f32x4*>(stf + at_rc(row, c));
+        if (col + 4 <= a.N) {
+          *reinterpret_cast<f32x4*>(dst) = v;
+        } else {
+          for (int q = 0; q < a.N - col; ++q) dst[q] = stf[at_rc(row, c) + q];
         }
       }
     }
+  }
 }
 
 // ----------------------------------------------------------------------------------- host side
@@ -290,6 +361,9 @@ int gemm_run(const char* who, bool glu, int bits, int adt, int sb, const MoeArgs
       return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": block_m 128 with 32-input scale blocks needs "
                                                              "4-byte aligned block_scale rows");
   }
+  // output rows are written 16 bytes at a time
+  if (a.s_om % (glu ? 8 : 4) || !aligned(a.out, 16))
+    return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": block_m 128 needs 16-byte aligned output rows");
   const int64_t x_rows = cdiv(a.num_slots, a.a_div);
   if (x_rows * a.s_xm * 2 > kOOR) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": activations over 2 GiB");
   const int64_t n_tiles = cdiv(a.N, glu ? gemm_cols<true>() : gemm_cols<false>());

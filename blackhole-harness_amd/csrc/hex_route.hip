@@ -105,6 +105,7 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const void* __restrict_
 constexpr int kAlignThreads = 1024;
 constexpr int kAlignWaves = kAlignThreads / kWave;
 constexpr int kAlignMaxExperts = 1024;
+constexpr int64_t kAlignSplit = 4096;     // slots above which the placement runs on many workgroups
 
 template <int IDT>
 __device__ __forceinline__ int64_t load_id(const void* p, int64_t i) {
@@ -137,29 +138,95 @@ __device__ int block_incl_scan(int v, int* wsum) {
   return r;
 }
 
-template <int IDT>
+// The lanes of a wave holding the same key as this lane (ballots over the key's nbits bits).
+__device__ __forceinline__ uint64_t match_key(int key, int nbits) {
+  uint64_t same = ~0ull;
+  for (int b = 0; b < nbits; ++b) {
+    const bool bit = (key >> b) & 1;
+    const uint64_t bal = __ballot(bit);
+    same &= bit ? bal : ~bal;
+  }
+  return same;
+}
+
+// Stable counting sort of the slots by expert, each expert's run padded to bm. Wave w owns the
+// contiguous slot range [w P, (w + 1) P): it counts its slots per expert (lanes with the same
+// key found by ballots over the key bits, so each key is counted once per 64-slot chunk), one
+// pass over the waves turns the counts into each wave's offset inside every expert's run, and
+// each wave then places its own range in order with no further workgroup barrier.
+// Without SCATTER the workgroup only counts (LDS atomics) and writes the block plan; the slots
+// are then placed by align_scatter_kernel, one workgroup per 1024 slots.
+template <int IDT, bool SCATTER>
 __global__ __launch_bounds__(kAlignThreads) void align_kernel(const void* __restrict__ ids, int64_t S, int32_t n,
                                                               int32_t bm, int64_t max_blocks,
                                                               int32_t* __restrict__ sorted_ids,
                                                               int32_t* __restrict__ expert_ids,
                                                               int32_t* __restrict__ npp) {
-  __shared__ int cnt[kAlignMaxExperts];      // slots per expert, then the running offset
+  __shared__ int cnt[kAlignMaxExperts];      // slots per expert
   __shared__ int start[kAlignMaxExperts];    // first padded row of the expert's run
-  __shared__ int wcnt[kAlignWaves][kAlignMaxExperts];
+  __shared__ int wcnt[kAlignWaves][kAlignMaxExperts];   // per wave: count, then offset in the run
   __shared__ int wsum[kAlignWaves];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  int nbits = 1;
+  while ((1 << nbits) <= n) ++nbits;          // keys in [0, n] (n marks "not placed")
+  const uint64_t below = (lane ? (~0ull >> (64 - lane)) : 0ull);
+  const int64_t per = (S + kAlignWaves - 1) / kAlignWaves;
+  const int64_t r0 = min(S, (int64_t)w * per), r1 = min(S, r0 + per);
+  // the keys of kBatch chunks of 64 slots from c0, loaded together (their loads overlap)
+  constexpr int kBatch = 16;
+  auto keys = [&](int64_t c0, int (&key)[kBatch]) {
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int64_t i = c0 + k * kWave + lane;
+      const int64_t e = i < r1 ? load_id<IDT>(ids, i) : -1;
+      key[k] = (e >= 0 && e < n) ? (int)e : n;
+    }
+  };
+  auto match = [&](int key) { return match_key(key, nbits); };
 
-  for (int e = tid; e < n; e += kAlignThreads) cnt[e] = 0;
-  __syncthreads();
-  for (int64_t i = tid; i < S; i += kAlignThreads) {
-    const int64_t e = load_id<IDT>(ids, i);
-    if (e >= 0 && e < n) atomicAdd(&cnt[e], 1);
+  if constexpr (SCATTER) {
+    for (int e = lane; e < n; e += kWave) wcnt[w][e] = 0;
+    __builtin_amdgcn_wave_barrier();
+    for (int64_t c0 = r0; c0 < r1; c0 += kBatch * kWave) {
+      int key[kBatch];
+      keys(c0, key);
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        const uint64_t same = match(key[k]);
+        if (key[k] < n && __popcll(same & below) == 0) wcnt[w][key[k]] += __popcll(same);
+        __builtin_amdgcn_wave_barrier();
+      }
+    }
+    __syncthreads();
+    for (int e = tid; e < n; e += kAlignThreads) {        // counts -> offsets over the waves
+      int acc = 0;
+      for (int v = 0; v < kAlignWaves; ++v) {
+        const int c = wcnt[v][e];
+        wcnt[v][e] = acc;
+        acc += c;
+      }
+      cnt[e] = acc;
+    }
+  } else {
+    for (int e = tid; e < n; e += kAlignThreads) cnt[e] = 0;
+    __syncthreads();
+    for (int64_t b0 = 0; b0 < S; b0 += kBatch * kAlignThreads) {
+      int64_t e[kBatch];
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        const int64_t i = b0 + k * kAlignThreads + tid;
+        e[k] = i < S ? load_id<IDT>(ids, i) : -1;
+      }
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k)
+        if (e[k] >= 0 && e[k] < n) atomicAdd(&cnt[e[k]], 1);
+    }
   }
   __syncthreads();
 
   // blocks per expert -> block ends (inclusive scan over experts, each thread a run of them)
-  const int per = (n + kAlignThreads - 1) / kAlignThreads;
-  const int e0 = tid * per, e1 = min(n, e0 + per);
+  const int pe = (n + kAlignThreads - 1) / kAlignThreads;
+  const int e0 = tid * pe, e1 = min(n, e0 + pe);
   int local = 0;
   for (int e = e0; e < e1; ++e) local += (cnt[e] + bm - 1) / bm;
   const int incl = block_incl_scan(local, wsum);
@@ -179,46 +246,89 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(const void* __rest
   for (int64_t b = used + tid; b < max_blocks; b += kAlignThreads) expert_ids[b] = -1;
   for (int64_t r = (int64_t)used * bm + tid; r < max_blocks * bm; r += kAlignThreads) sorted_ids[r] = (int32_t)S;
   if (tid == 0) npp[0] = used * bm;
-  for (int e = tid; e < n; e += kAlignThreads) cnt[e] = 0;   // now the running offset
-  __syncthreads();
+  if constexpr (!SCATTER) return;
 
-  // stable scatter, one chunk of 1024 slots at a time
-  int nbits = 1;
-  while ((1 << nbits) <= n) ++nbits;          // ids in [0, n] (n marks "not placed")
-  const uint64_t below = (lane ? (~0ull >> (64 - lane)) : 0ull);
-  for (int64_t c0 = 0; c0 < S; c0 += kAlignThreads) {
-    for (int i = tid; i < kAlignWaves * n; i += kAlignThreads) wcnt[i / n][i % n] = 0;
-    const int64_t i = c0 + tid;
-    int key = n;
-    if (i < S) {
-      const int64_t e = load_id<IDT>(ids, i);
-      if (e >= 0 && e < n) key = (int)e;
-    }
-    uint64_t same = ~0ull;
-    for (int b = 0; b < nbits; ++b) {
-      const bool bit = (key >> b) & 1;
-      const uint64_t bal = __ballot(bit);
-      same &= bit ? bal : ~bal;
-    }
-    const int rank = __popcll(same & below);
-    __syncthreads();
-    if (key < n && rank == 0) wcnt[w][key] = __popcll(same);
-    __syncthreads();
-    for (int e = tid; e < n; e += kAlignThreads) {       // exclusive prefix over the waves
-      int acc = cnt[e];
-      for (int v = 0; v < kAlignWaves; ++v) {
-        const int c = wcnt[v][e];
-        wcnt[v][e] = acc;
-        acc += c;
+  // each wave places its range, chunk by chunk in slot order: a lane's row is its expert's
+  // run start + the wave's offset in that run + its rank among the chunk's lanes of the expert;
+  // the key's lowest lane then moves the wave's offset on (after every lane has read it)
+  for (int64_t c0 = r0; c0 < r1; c0 += kBatch * kWave) {
+    int key[kBatch];
+    keys(c0, key);
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int64_t i = c0 + k * kWave + lane;
+      const uint64_t same = match(key[k]);
+      const int rank = __popcll(same & below);
+      if (key[k] < n) {
+        const int64_t pos = (int64_t)start[key[k]] + wcnt[w][key[k]] + rank;
+        if (pos < max_blocks * bm) sorted_ids[pos] = (int32_t)i;
       }
-      cnt[e] = acc;
+      __builtin_amdgcn_wave_barrier();
+      if (key[k] < n && rank == 0) wcnt[w][key[k]] += __popcll(same);
+      __builtin_amdgcn_wave_barrier();
     }
-    __syncthreads();
-    if (key < n) {
-      const int64_t pos = (int64_t)start[key] + wcnt[w][key] + rank;
-      if (pos < max_blocks * bm) sorted_ids[pos] = (int32_t)i;
+  }
+}
+
+// Places the slots of chunk blockIdx.x (1024 slots) after align_kernel<IDT, false> wrote the
+// block plan: the chunk's slots of each expert go after the expert's slots in earlier chunks
+// (counted again here), in slot order (per wave by ballot rank, then over the waves).
+template <int IDT>
+__global__ __launch_bounds__(kAlignThreads) void align_scatter_kernel(const void* __restrict__ ids, int64_t S,
+                                                                      int32_t n, int32_t bm, int64_t max_blocks,
+                                                                      int32_t* __restrict__ sorted_ids,
+                                                                      const int32_t* __restrict__ expert_ids,
+                                                                      const int32_t* __restrict__ npp) {
+  __shared__ int pre[kAlignMaxExperts];      // the expert's slots in earlier chunks
+  __shared__ int start[kAlignMaxExperts];    // first padded row of the expert's run
+  __shared__ int wcnt[kAlignWaves][kAlignMaxExperts];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  int nbits = 1;
+  while ((1 << nbits) <= n) ++nbits;
+  const uint64_t below = (lane ? (~0ull >> (64 - lane)) : 0ull);
+  const int64_t c0 = (int64_t)blockIdx.x * kAlignThreads;
+  for (int e = tid; e < n; e += kAlignThreads) pre[e] = 0;
+  for (int e = lane; e < n; e += kWave) wcnt[w][e] = 0;
+  __syncthreads();
+  constexpr int kBatch = 16;
+  for (int64_t b0 = 0; b0 < c0; b0 += kBatch * kAlignThreads) {
+    int64_t e[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int64_t i = b0 + k * kAlignThreads + tid;
+      e[k] = i < c0 ? load_id<IDT>(ids, i) : -1;
     }
-    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k)
+      if (e[k] >= 0 && e[k] < n) atomicAdd(&pre[e[k]], 1);
+  }
+  const int used = npp[0] / bm;
+  for (int b = tid; b < used; b += kAlignThreads) {
+    const int e = expert_ids[b];
+    if (e >= 0 && e < n && (b == 0 || expert_ids[b - 1] != e)) start[e] = b * bm;
+  }
+  const int64_t i = c0 + tid;
+  int key = n;
+  if (i < S) {
+    const int64_t e = load_id<IDT>(ids, i);
+    if (e >= 0 && e < n) key = (int)e;
+  }
+  const uint64_t same = match_key(key, nbits);
+  const int rank = __popcll(same & below);
+  if (key < n && rank == 0) wcnt[w][key] = __popcll(same);
+  __syncthreads();
+  for (int e = tid; e < n; e += kAlignThreads) {        // offsets: earlier chunks, then earlier waves
+    int acc = pre[e];
+    for (int v = 0; v < kAlignWaves; ++v) {
+      const int c = wcnt[v][e];
+      wcnt[v][e] = acc;
+      acc += c;
+    }
+  }
+  __syncthreads();
+  if (key < n) {
+    const int64_t pos = (int64_t)start[key] + wcnt[w][key] + rank;
+    if (pos < max_blocks * bm) sorted_ids[pos] = (int32_t)i;
   }
 }
 
@@ -284,12 +394,25 @@ extern "C" int bh_hex_align(const void* ids, int32_t ids_dtype, int64_t S, int32
   const int64_t max_blocks = bh_hex_align_max_blocks(S, n_experts, block_m);
   if (max_blocks * block_m > (int64_t)INT32_MAX) return fail(BH_HEX_ERR_VALUE, "bh_hex_align: plan too large");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (ids_dtype == BH_HEX_I64)
-    hipLaunchKernelGGL((align_kernel<BH_HEX_I64>), dim3(1), dim3(kAlignThreads), 0, st, ids, S, n_experts, block_m,
-                       max_blocks, sorted_ids, expert_ids, npp);
-  else
-    hipLaunchKernelGGL((align_kernel<BH_HEX_I32>), dim3(1), dim3(kAlignThreads), 0, st, ids, S, n_experts, block_m,
-                       max_blocks, sorted_ids, expert_ids, npp);
+  // up to kAlignSplit slots one workgroup does everything; above, it writes the block plan and
+  // one workgroup per 1024 slots places them
+  const bool split = S > kAlignSplit;
+  const dim3 chunks((unsigned)cdiv(S, kAlignThreads));
+#define BH_ALIGN(IDT)                                                                                              \
+  do {                                                                                                             \
+    if (split) {                                                                                                   \
+      hipLaunchKernelGGL((align_kernel<IDT, false>), dim3(1), dim3(kAlignThreads), 0, st, ids, S, n_experts, block_m, \
+                         max_blocks, sorted_ids, expert_ids, npp);                                                 \
+      hipLaunchKernelGGL((align_scatter_kernel<IDT>), chunks, dim3(kAlignThreads), 0, st, ids, S, n_experts, block_m, \
+                         max_blocks, sorted_ids, expert_ids, npp);                                                 \
+    } else {                                                                                                       \
+      hipLaunchKernelGGL((align_kernel<IDT, true>), dim3(1), dim3(kAlignThreads), 0, st, ids, S, n_experts, block_m,  \
+                         max_blocks, sorted_ids, expert_ids, npp);                                                 \
+    }                                                                                                              \
+  } while (0)
+  if (ids_dtype == BH_HEX_I64) BH_ALIGN(BH_HEX_I64);
+  else BH_ALIGN(BH_HEX_I32);
+#undef BH_ALIGN
   return check_launch("bh_hex_align");
 }
 

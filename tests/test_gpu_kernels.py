@@ -107,7 +107,9 @@ def test_dequant_all_places_experts():
                                              (8, 4, 4, False, torch.int32), (37, 5, 4, False, torch.int64),
                                              (128, 96, 16, False, torch.int64), (512, 96, 16, False, torch.int32),
                                              (2048, 96, 32, True, torch.int64), (3000, 1000, 16, False, torch.int64),
-                                             (32768, 96, 64, False, torch.int64), (40000, 128, 16, True, torch.int32)])
+                                             (32768, 96, 64, False, torch.int64), (40000, 128, 16, True, torch.int32),
+                                             (4096, 96, 128, False, torch.int64), (4097, 96, 128, True, torch.int64),
+                                             (33000, 96, 128, True, torch.int32), (20000, 1000, 128, True, torch.int64)])
 def test_align_bit_exact(S, n, bm, skew, idt):
     say(f"align S={S} n={n} bm={bm} skew={skew} {idt}")
     rng = np.random.default_rng(S + n + bm)

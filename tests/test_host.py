@@ -65,7 +65,9 @@ def test_default_config_and_env(monkeypatch):
     assert hm._tile_from({"BLOCK_M": 64, "BLOCK_N": 128}) == 64
     assert hm._tile_from({"BLOCK_M": 128, "BLOCK_N": 128}) == 128
     assert hm._tile_from({"BLOCK_M": 24}) == 32
-    assert hm._fit_tile(128, 768) == 128 and hm._fit_tile(128, 160) == 64 and hm._fit_tile(32, 160) == 32
+    assert hm._fit_tile(128, 768, 2048, False) == 128 and hm._fit_tile(128, 160, 2048, False) == 64
+    assert hm._fit_tile(128, 2048, 100, True) == 64 and hm._fit_tile(128, 2048, 100, False) == 128
+    assert hm._fit_tile(32, 160, 99, True) == 32
 
 
 def test_kernels_refuse_cpu_tensors():
