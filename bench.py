@@ -333,7 +333,7 @@ def rocprof_summary(dirs: list[str]) -> str:
                 agg.setdefault(key, []).append(float(r["Counter_Value"]))
             out.append(f"## counters, mean per dispatch ({d})")
             for (k, c), v in sorted(agg.items()):
-                if "hex_moe" in k or "align_kernel" in k or "moe_reduce" in k or "bitwise_not" in k:
+                if any(s in k for s in ("hex_moe", "hex_gemm", "align_", "moe_reduce", "bitwise_not")):
                     out.append(f"{k:<112} {c:<12} {sum(v) / len(v):>14.1f}  (n={len(v)})")
                 counters.setdefault(c, {})[k] = v
     if "FETCH_SIZE" in counters and "WRITE_SIZE" in counters:

@@ -170,7 +170,8 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(const void* __rest
   int nbits = 1;
   while ((1 << nbits) <= n) ++nbits;          // keys in [0, n] (n marks "not placed")
   const uint64_t below = (lane ? (~0ull >> (64 - lane)) : 0ull);
-  const int64_t per = (S + kAlignWaves - 1) / kAlignWaves;
+  // whole 64-slot chunks per wave (a small batch leaves the later waves empty)
+  const int64_t per = ((S + kAlignWaves - 1) / kAlignWaves + kWave - 1) / kWave * kWave;
   const int64_t r0 = min(S, (int64_t)w * per), r1 = min(S, r0 + per);
   // the keys of kBatch chunks of 64 slots from c0, loaded together (their loads overlap)
   constexpr int kBatch = 16;
@@ -192,6 +193,7 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(const void* __rest
       keys(c0, key);
 #pragma unroll
       for (int k = 0; k < kBatch; ++k) {
+        if (c0 + k * kWave >= r1) break;                 // (uniform: the wave's range ends)
         const uint64_t same = match(key[k]);
         if (key[k] < n && __popcll(same & below) == 0) wcnt[w][key[k]] += __popcll(same);
         __builtin_amdgcn_wave_barrier();
@@ -256,6 +258,7 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(const void* __rest
     keys(c0, key);
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
+      if (c0 + k * kWave >= r1) break;                   // (uniform: the wave's range ends)
       const int64_t i = c0 + k * kWave + lane;
       const uint64_t same = match(key[k]);
       const int rank = __popcll(same & below);
