@@ -421,14 +421,18 @@ def main(argv=None) -> int:
             log(f"  T={Ts}: {r['ms_per_step'] * 1e3:.1f} us/layer, {r['hbm_gbps']:.0f} GB/s")
         del copies
         torch.cuda.empty_cache()
-        pf = build_tiers(CONFIGS[3], a.block, 2, dev)
-        r, _ = run_layer(CONFIGS[3], pf, 4096, 16, 4, a.block, breakdown=False)
-        sweep["config3_T4096"] = {kk: r[kk] for kk in ("ms_per_step", "tokens_per_s", "mfma_frac", "hbm_gbps",
-                                                        "unique_experts")}
-        log(f"  config3 T=4096: {r['ms_per_step']:.2f} ms/layer, MFMA {r['mfma_frac'] * 100:.1f}% of bf16 peak")
+        keys = ("ms_per_step", "tokens_per_s", "mfma_frac", "hbm_gbps", "hbm_frac", "unique_experts")
+        # the other configs: (config, resident copies, token batches, timed calls per batch)
+        for c, n_copies, batches, steps in ((3, 2, (4096,), 16), (4, 4, (256,), 100), (5, 8, (16, 2048), 32)):
+            layers = build_tiers(CONFIGS[c], a.block, n_copies, dev)
+            for Ts in batches:
+                r, _ = run_layer(CONFIGS[c], layers, Ts, steps, a.warmup, a.block, breakdown=False)
+                sweep[f"config{c}_T{Ts}"] = {kk: r[kk] for kk in keys}
+                log(f"  config{c} T={Ts}: {r['ms_per_step'] * 1e3:.1f} us/layer, {r['hbm_gbps']:.0f} GB/s "
+                    f"({r['hbm_frac'] * 100:.1f}% of HBM), MFMA {r['mfma_frac'] * 100:.1f}% of bf16 peak")
+            del layers
+            torch.cuda.empty_cache()
         copies = None
-        del pf
-        torch.cuda.empty_cache()
 
     if a.copy_calibration:
         src = torch.empty(128 << 20, dtype=torch.int16, device=dev).random_()

@@ -68,8 +68,10 @@ __device__ __forceinline__ void fp8x4_nb(uint32_t w, float f[4]) {
 // Eight operands (two per dword, K order) for the codes of one 24/32-bit field, from a pair
 // table in LDS: entry p holds (level[p & (L-1)], level[p >> bits]) in the activation dtype,
 // one copy per lane slot, at byte (p << 8) | cb.
-template <int BITS>
+// ES = log2 of an entry's bytes (8: 64 copies; 7: 32 copies, 3-bit tables only).
+template <int BITS, int ES = 8>
 __device__ __forceinline__ u32x4 lookup8(uint32_t f, uint32_t cb, const uint32_t* tab) {
+  static_assert(ES == 8 || (BITS == 3 && ES == 7), "4-bit tables have 64 copies");
   const char* base = reinterpret_cast<const char*>(tab);
   u32x4 b;
 #pragma unroll
@@ -78,10 +80,11 @@ __device__ __forceinline__ u32x4 lookup8(uint32_t f, uint32_t cb, const uint32_t
     if constexpr (BITS == 4) {
       addr = __builtin_amdgcn_perm(f, cb, 0x0C0C0000u | ((4u + j) << 8));  // byte j << 8 | cb
     } else {
-      // ((f >> 6 j) & 63) << 8 | cb as one shift and one v_and_or_b32 (the compiler's own
+      // ((f >> 6 j) & 63) << ES | cb as one shift and one v_and_or_b32 (the compiler's own
       // form is a shift, a mask and an add)
-      const uint32_t sh = j == 0 ? f << 8 : j == 1 ? f << 2 : j == 2 ? f >> 4 : f >> 10;
-      asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(addr) : "v"(sh), "s"(0x3F00u), "v"(cb));
+      const int d = ES - 6 * j;
+      const uint32_t sh = d >= 0 ? f << d : f >> -d;
+      asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(addr) : "v"(sh), "s"(63u << ES), "v"(cb));
     }
     b[j] = *reinterpret_cast<const uint32_t*>(base + addr);
   }

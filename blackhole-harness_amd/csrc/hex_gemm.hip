@@ -31,14 +31,21 @@
 
 namespace bh {
 
-constexpr int kGThreads = 512;          // 8 waves, 32 weight rows each
-constexpr int kGWaves = kGThreads / kWave;
+// Weight-row groups of 16 per wave: 4 at 3 bits (4 waves per workgroup, two workgroups per
+// compute unit, every activation fragment read feeds 4 groups), 2 at 4 bits (8 waves: the
+// 64 KB 4-bit table leaves room for one workgroup, whose waves then cover each other's latency).
+constexpr int kMaxNG = 4, kMaxChunks = 8;
+template <int BITS>
+struct GemmShape {
+  static constexpr int NG = BITS == 3 ? 4 : 2;     // weight-row groups of 16 per wave
+  static constexpr int WAVES = 16 / NG;            // waves of a workgroup (256 weight rows)
+  static constexpr int THREADS = WAVES * kWave;
+  static constexpr int CHUNKS = 32 / WAVES;        // 1 KB chunks of a step's activation tile per wave
+};
 constexpr int kGM = 128;                // slots of a tile: one expert block of the plan
 constexpr int kGK = 128;                // inputs per pipeline step
 constexpr int kGTile = kGM * kGK / 2;   // dwords of one step's activation tile
 constexpr int kXcds = 8;
-
-constexpr int kTileLoads = 4;           // buffer loads per lane of one step's activation tile
 
 // s_waitcnt operand that waits until at most n vector-memory loads are in flight (gfx9:
 // vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima)
@@ -48,19 +55,30 @@ template <bool GLU>
 constexpr int gemm_cols() { return GLU ? 128 : 256; }   // outputs of a tile
 
 template <int BITS, int ADT, bool GLU, int SB>
-__global__ __launch_bounds__(kGThreads) void hex_gemm_kernel(MoeArgs a, int n_tiles) {
+__global__ __launch_bounds__(512, 2) void hex_gemm_kernel(MoeArgs a, int n_tiles) {
+  // (arrays below are sized by the non-dependent maxima kMaxNG / kMaxChunks: with sizes that
+  // depend on BITS this compiler emits no host-side launch stub for the kernel)
+  constexpr int kNG = GemmShape<BITS>::NG;
+  constexpr int kGWaves = GemmShape<BITS>::WAVES;
+  constexpr int kGThreads = GemmShape<BITS>::THREADS;
+  constexpr int kChunks = GemmShape<BITS>::CHUNKS;
   constexpr int L = 1 << BITS;
   constexpr int NPAIR = 1 << (2 * BITS);
   constexpr int NM = GLU ? 2 : 1;
   constexpr int BLKB = BITS * 4;               // bytes of one 32-input block of one row
   using W = typename std::conditional<BITS == 4, u32x4, u32x3>::type;
+  // Pair-table copies per entry: 64 at 4 bits; 32 at 3 bits, so that two workgroups fit in a
+  // compute unit's LDS (a wave's table reads go to the banks in two halves of 32 lanes, so 32
+  // copies keep down's reads conflict-free; GLU's gate and up tables get 16 copies each).
+  constexpr int TC = BITS == 3 ? 32 : 64;
+  constexpr int ES = BITS == 3 ? 7 : 8;          // log2 of an entry's bytes
   // Activation ring depth: tiles are loaded one step ahead of the math, as are the weight
   // words (two register sets). (Two steps ahead measured no faster.)
   constexpr int D = 2;
   // One LDS object with the pair table first: the table sits at LDS address 0, so table reads
   // need no base add (the 16-bit instruction offset cannot hold a base past 64 KB).
   struct Lds {
-    uint32_t tab[NPAIR * 64];
+    uint32_t tab[NPAIR * TC];
     uint32_t atile[D][kGTile];   // the activation tile ring
     int slots[kGM];
     float slot_w[GLU ? 1 : kGM];
@@ -103,42 +121,46 @@ __global__ __launch_bounds__(kGThreads) void hex_gemm_kernel(MoeArgs a, int n_ti
   }
   __syncthreads();
 
-  // ---- load offsets. Activations: chunk i * 8 + wave of a step's tile is m-tile
-  // 2 i + wave / 4, k-slice wave % 4; lane (ln, lg) reads inputs 32 (wave % 4) + 8 lg .. + 7 of
-  // slot row 16 m-tile + ln.
+  // ---- load offsets. Activations: chunk c = i * waves + wave of a step's tile is m-tile c / 4,
+  // k-slice c % 4; lane (ln, lg) reads inputs 32 (c % 4) + 8 lg .. + 7 of slot row
+  // 16 (c / 4) + ln.
   const int x_rows = (int)((a.num_slots + a.a_div - 1) / a.a_div);
   const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(a.x, (int64_t)x_rows * a.s_xm * 2);
-  int xo[4];
+  int xo[kMaxChunks];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int s = slots[(2 * i + (wave >> 2)) * 16 + ln];
-    xo[i] = s < a.num_slots ? (int)((int64_t)(s / a.a_div) * a.s_xm * 2) + ((wave & 3) * 32 + lg * 8) * 2 : kOOR;
+  for (int i = 0; i < kChunks; ++i) {
+    const int c = i * kGWaves + wave;
+    const int s = slots[(c >> 2) * 16 + ln];
+    xo[i] = s < a.num_slots ? (int)((int64_t)(s / a.a_div) * a.s_xm * 2) + ((c & 3) * 32 + lg * 8) * 2 : kOOR;
   }
-  // Weights: the wave's two groups of 16 rows; lane (ln, lg) reads block lg of the step of row
-  // ln. Down: rows 256 nt + 32 wave + 16 g. GLU: gate (g = 0) and up (g = 1) rows 128 nt + 16 wave.
-  int vw[2], vb[2];
-  uint32_t cb[2];
-  __amdgpu_buffer_rsrc_t rw[2], rb[2];
+  // Weights: the wave's groups of 16 rows; lane (ln, lg) reads block lg of the step of row ln.
+  // Down: rows 256 nt + 16 (NG wave + g). GLU: group g is gate (g < NG/2) or up, half h = g % (NG/2):
+  // rows 128 nt + 16 (NG/2 wave + h) of both, so a lane holds gate and up of the same outputs.
+  constexpr int HG = kNG / 2;
+  int vw[kMaxNG], vb[kMaxNG];
+  uint32_t cb[kMaxNG];
+  __amdgpu_buffer_rsrc_t rw[kMaxNG], rb[kMaxNG];
 #pragma unroll
-  for (int g = 0; g < 2; ++g) {
-    const bh_hex_proj& w = (GLU && g == 1) ? a.w1 : a.w0;
+  for (int g = 0; g < kNG; ++g) {
+    const int m = GLU ? g / HG : 0;
+    const bh_hex_proj& w = m ? a.w1 : a.w0;
     rw[g] = buffer_rsrc(w.idx + (int64_t)e * w.s_ie, (int64_t)a.N * w.s_in * 4);
     rb[g] = buffer_rsrc(w.block_scale + (int64_t)e * w.s_be, (int64_t)a.N * w.s_bn);
-    const int n = GLU ? nt * 128 + wave * 16 + ln : nt * 256 + wave * 32 + g * 16 + ln;
+    const int n = GLU ? nt * 128 + (wave * HG + g % HG) * 16 + ln : nt * 256 + (wave * kNG + g) * 16 + ln;
     vw[g] = n < a.N ? (int)((int64_t)n * w.s_in * 4) + lg * BLKB : kOOR;
     vb[g] = n < a.N ? (int)((int64_t)n * w.s_bn) : kOOR;
-    cb[g] = GLU ? (uint32_t)g * 128u + (lane & 31u) * 4u : lane * 4u;
+    cb[g] = GLU ? (uint32_t)m * (TC * 2) + (lane & (TC / 2 - 1)) * 4u : (lane & (TC - 1)) * 4u;
   }
 
   // a step's activation tile, straight into LDS (buffer loads with the LDS bit): chunk
-  // i * 8 + wave, 16 bytes per lane at lane * 16. Padding rows read out of range.
+  // i * waves + wave, 16 bytes per lane at lane * 16. Padding rows read out of range.
   auto load_a1 = [&](int st, int i, uint32_t* at) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)(at + (i * kGWaves + wave) * 256),
                                              16, xo[i] + st * (kGK * 2), 0, 0, 0);
   };
   auto load_a = [&](int st, uint32_t* at) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) load_a1(st, i, at);
+    for (int i = 0; i < kChunks; ++i) load_a1(st, i, at);
   };
   auto load_w1 = [&](int st, int g, W& w, uint32_t& sc) {
     if constexpr (BITS == 4) ld_x4<0>(w, rw[g], vw[g] + st * 4 * BLKB);
@@ -146,34 +168,34 @@ __global__ __launch_bounds__(kGThreads) void hex_gemm_kernel(MoeArgs a, int n_ti
     if constexpr (SB == 4) ld_u8<0>(sc, rb[g], vb[g] + st);
     else ld_x1<0>(sc, rb[g], vb[g] + 4 * st);
   };
-  auto load_w = [&](int st, W (&ws)[2], uint32_t (&sc)[2]) {
+  auto load_w = [&](int st, W (&ws)[kMaxNG], uint32_t (&sc)[kMaxNG]) {
 #pragma unroll
-    for (int g = 0; g < 2; ++g) load_w1(st, g, ws[g], sc[g]);
+    for (int g = 0; g < kNG; ++g) load_w1(st, g, ws[g], sc[g]);
   };
 
-  W ws[2][2];                     // weight words of this step and the next (ping-pong)
-  uint32_t ss[2][2];
+  W ws[2][kMaxNG];                   // weight words of this step and the next (ping-pong)
+  uint32_t ss[2][kMaxNG];
   load_w(0, ws[0], ss[0]);
 #pragma unroll
   for (int d = 0; d < D - 1; ++d) load_a(d < nst ? d : nst - 1, sm.atile[d]);
 
-  // ---- the expert's pair table: entry p = (level[p & (L-1)], level[p >> bits]), 64 copies
-  // (GLU: copies 0-31 gate, 32-63 up)
+  // ---- the expert's pair table: entry p = (level[p & (L-1)], level[p >> bits]), TC copies
+  // (GLU: the first half gate, the second up)
 #pragma unroll
-  for (int i = 0; i < NPAIR * 16 / kGThreads; ++i) {
+  for (int i = 0; i < NPAIR * TC / 4 / kGThreads; ++i) {
     const int base = (i * kGThreads + tid) * 4;
-    const int p = base >> 6, t = GLU ? (base & 63) >> 5 : 0;
+    const int p = base / TC, t = GLU ? (base % TC) / (TC / 2) : 0;
     const uint32_t v = (uint32_t)lvs[t][p & (L - 1)] | ((uint32_t)lvs[t][p >> BITS] << 16);
     *reinterpret_cast<u32x4*>(&tab[base]) = u32x4{v, v, v, v};
   }
-  __builtin_amdgcn_s_waitcnt(vm_wait(kTileLoads * (D - 2)));   // step 0's loads have landed
+  __builtin_amdgcn_s_waitcnt(vm_wait(kChunks * (D - 2)));   // step 0's loads have landed
   __syncthreads();
 
-  f32x4 acc[8][2];                       // [m-tile][group]
+  f32x4 acc[8][kMaxNG];                     // [m-tile][group]
 #pragma unroll
   for (int j = 0; j < 8; ++j)
 #pragma unroll
-    for (int g = 0; g < 2; ++g) acc[j][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int g = 0; g < kNG; ++g) acc[j][g] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // One step (phase P = st % D): the loads of step st + D - 1 first (into the ring stage and
   // register set that step st - 1 used; past the end the last step repeats, so every load
@@ -184,8 +206,8 @@ __global__ __launch_bounds__(kGThreads) void hex_gemm_kernel(MoeArgs a, int n_ti
   auto step = [&](int st, auto phase) {
     constexpr int P = decltype(phase)::value;
     const uint32_t* at = sm.atile[st % D];
-    const W (&cw)[2] = ws[P];
-    const uint32_t (&cs)[2] = ss[P];
+    const W (&cw)[kMaxNG] = ws[P];
+    const uint32_t (&cs)[kMaxNG] = ss[P];
     const int sw = st + 1 < nst ? st + 1 : st;
     const int sa = st + D - 1 < nst ? st + D - 1 : nst - 1;
     uint32_t* const an = sm.atile[(st + D - 1) % D];
@@ -193,61 +215,63 @@ __global__ __launch_bounds__(kGThreads) void hex_gemm_kernel(MoeArgs a, int n_ti
     // the next step's loads spread over the m-tiles: issued back to back at the start of a
     // step, 64 loads per compute unit hold every wave at the memory pipe before its MFMAs)
     __builtin_amdgcn_sched_barrier(0);
-    u32x4 bq[2][4];
-    float f[2][SB == 4 ? 1 : 4];
+    // the step's code fields and scales; the operands are looked up per half step (64 inputs,
+    // k-slices 2 hq and 2 hq + 1), which keeps half the B operands live
+    uint32_t r[kMaxNG][4];
+    float f[kMaxNG][4];
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      uint32_t r[4];
-      fields<BITS>(cw[g], r);            // r[q]: block 4 st + q
-#pragma unroll
-      for (int q = 0; q < 4; ++q) bq[g][q] = lookup8<BITS>(r[q], cb[g], tab);
-      if constexpr (SB == 4) f[g][0] = fp8x1_nb(cs[g]);
-      else fp8x4_nb(cs[g], f[g]);
+    for (int g = 0; g < kNG; ++g) {
+      fields<BITS>(cw[g], r[g]);         // r[g][q]: block 4 st + q
+      fp8x4_nb(cs[g], f[g]);             // (at 128-input blocks the step's scale is byte 0; the
+                                         // four-byte form also keeps the register allocation sane)
     }
-    auto afrag = [&](int j, u32x4 (&av)[4]) {
+    auto afrag = [&](int j, int hq, u32x4 (&av)[2]) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) av[q] = *reinterpret_cast<const u32x4*>(at + ((j * 4 + q) * 64 + lane) * 4);
+      for (int q = 0; q < 2; ++q)
+        av[q] = *reinterpret_cast<const u32x4*>(at + ((j * 4 + 2 * hq + q) * 64 + lane) * 4);
     };
-    u32x4 av[2][4];
-    f32x4 part[2][2];
-    afrag(0, av[0]);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      __builtin_amdgcn_sched_barrier(0);
-      if (j + 1 < 8) afrag(j + 1, av[(j + 1) & 1]);
-      if (j < 2) load_w1(sw, j, ws[1 - P][j], ss[1 - P][j]);
-      else if (j < 6) load_a1(sa, j - 2, an);
-      __builtin_amdgcn_sched_barrier(0);
-      const u32x4 (&x)[4] = av[j & 1];
-      if constexpr (SB == 4) {
-        f32x4 p0 = f32x4{0.f, 0.f, 0.f, 0.f}, p1 = p0;
+    for (int hq = 0; hq < 2; ++hq) {
+      u32x4 bq[kMaxNG][2];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          p0 = mfma16x16x32<ADT>(x[q], bq[0][q], p0);
-          p1 = mfma16x16x32<ADT>(x[q], bq[1][q], p1);
-        }
-        part[j & 1][0] = p0;
-        part[j & 1][1] = p1;
-        if (j > 0) {
-          acc[j - 1][0] += part[(j - 1) & 1][0] * f[0][0];
-          acc[j - 1][1] += part[(j - 1) & 1][1] * f[1][0];
-        }
-      } else {
+      for (int g = 0; g < kNG; ++g)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const f32x4 z = f32x4{0.f, 0.f, 0.f, 0.f};
-          acc[j][0] += mfma16x16x32<ADT>(x[q], bq[0][q], z) * f[0][q];
-          acc[j][1] += mfma16x16x32<ADT>(x[q], bq[1][q], z) * f[1][q];
+        for (int q = 0; q < 2; ++q) bq[g][q] = lookup8<BITS, ES>(r[g][2 * hq + q], cb[g], tab);
+      u32x4 av[2][2];
+      afrag(0, hq, av[0]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (j + 1 < 8) afrag(j + 1, hq, av[(j + 1) & 1]);
+        // the next step's loads: words in the first half step, tile chunks in the second
+        const int t = hq * 8 + j;
+        if (t < kNG) load_w1(sw, t, ws[1 - P][t], ss[1 - P][t]);
+        else if (t >= 8 && t < 8 + kChunks) load_a1(sa, t - 8, an);
+        __builtin_amdgcn_sched_barrier(0);
+        const u32x4 (&x)[2] = av[j & 1];
+        if constexpr (SB == 4) {
+          // the block's scale times the partial of each half step (one 128-input block per step)
+          f32x4 p[kMaxNG];
+#pragma unroll
+          for (int g = 0; g < kNG; ++g) p[g] = mfma16x16x32<ADT>(x[0], bq[g][0], f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+          for (int g = 0; g < kNG; ++g) p[g] = mfma16x16x32<ADT>(x[1], bq[g][1], p[g]);
+#pragma unroll
+          for (int g = 0; g < kNG; ++g) acc[j][g] += p[g] * f[g][0];
+        } else {
+          // each k-slice partial times its block's scale
+#pragma unroll
+          for (int q = 0; q < 2; ++q)
+#pragma unroll
+            for (int g = 0; g < kNG; ++g)
+              acc[j][g] += mfma16x16x32<ADT>(x[q], bq[g][q], f32x4{0.f, 0.f, 0.f, 0.f}) * f[g][2 * hq + q];
         }
       }
     }
-    if constexpr (SB == 4) {
-      acc[7][0] += part[1][0] * f[0][0];
-      acc[7][1] += part[1][1] * f[1][0];
-    }
+
     // step st + 1's words and tile have landed (the tile loads issued after its words, for
     // D - 2 steps further on, stay in flight)
-    __builtin_amdgcn_s_waitcnt(vm_wait(kTileLoads * (D - 2)));
+    __builtin_amdgcn_s_waitcnt(vm_wait(kChunks * (D - 2)));
     __syncthreads();                     // every wave's chunks of the next tile; this tile is free
   };
   // pairs of steps (the register set of a step is a compile-time constant), then the last one
@@ -271,9 +295,12 @@ __global__ __launch_bounds__(kGThreads) void hex_gemm_kernel(MoeArgs a, int n_ti
     for (int j = 0; j < 8; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float gt = acc[j][0][r] * es0;
-        const float hv = gt * __builtin_amdgcn_rcpf(1.0f + __expf(-gt)) * (acc[j][1][r] * es1);
-        st16[(j * 16 + 4 * lg + r) * RS + wave * 16 + ln] = (uint16_t)to_bits<ADT>(hv);
+#pragma unroll
+        for (int h = 0; h < HG; ++h) {
+          const float gt = acc[j][h][r] * es0;
+          const float hv = gt * __builtin_amdgcn_rcpf(1.0f + __expf(-gt)) * (acc[j][HG + h][r] * es1);
+          st16[(j * 16 + 4 * lg + r) * RS + (wave * HG + h) * 16 + ln] = (uint16_t)to_bits<ADT>(hv);
+        }
       }
     __syncthreads();
     // 16 threads per row, 8 outputs (16 bytes) each
@@ -305,7 +332,7 @@ __global__ __launch_bounds__(kGThreads) void hex_gemm_kernel(MoeArgs a, int n_ti
           const int row = j * 16 + 4 * lg + r;           // within the half
           const float w = slot_w[h * 64 + row];
 #pragma unroll
-          for (int g = 0; g < 2; ++g) stf[at_rc(row, wave * 32 + g * 16 + ln)] = acc[h * 4 + j][g][r] * es0 * w;
+          for (int g = 0; g < kNG; ++g) stf[at_rc(row, (wave * kNG + g) * 16 + ln)] = acc[h * 4 + j][g][r] * es0 * w;
         }
       __syncthreads();
       // 64 threads per row, 4 outputs (16 bytes) each
@@ -330,8 +357,9 @@ __global__ __launch_bounds__(kGThreads) void hex_gemm_kernel(MoeArgs a, int n_ti
 
 template <int BITS, int ADT, bool GLU>
 static void gemm_sb(int sb, dim3 grid, hipStream_t st, const MoeArgs& a, int n_tiles) {
-  if (sb == 1) hipLaunchKernelGGL((hex_gemm_kernel<BITS, ADT, GLU, 1>), grid, dim3(kGThreads), 0, st, a, n_tiles);
-  else hipLaunchKernelGGL((hex_gemm_kernel<BITS, ADT, GLU, 4>), grid, dim3(kGThreads), 0, st, a, n_tiles);
+  const dim3 block(GemmShape<BITS>::THREADS);
+  if (sb == 1) hipLaunchKernelGGL((hex_gemm_kernel<BITS, ADT, GLU, 1>), grid, block, 0, st, a, n_tiles);
+  else hipLaunchKernelGGL((hex_gemm_kernel<BITS, ADT, GLU, 4>), grid, block, 0, st, a, n_tiles);
 }
 
 template <bool GLU>
