@@ -63,9 +63,11 @@ typedef struct bh_hex_proj {
 } bh_hex_proj;
 
 /* Tile choice of the fused kernels (the config dict of hex_moe.py:264-283, CDNA4 terms):
- * block_m slots per expert block (16, 32 or 64). block_n, the output rows of one work item
- * (16 per wave of a 16-wave workgroup), must be 256; k_split must be 1 (the inputs of an item
- * are split between workgroups by the kernels themselves). */
+ * block_m slots per expert block: 16, 32 or 64 select the decode kernels (weight-streaming,
+ * an item's inputs split between workgroups), 128 the prefill kernels (one workgroup per
+ * 128-slot block and tile of 256 weight rows; n_in must be a multiple of 128 and output rows
+ * 16-byte aligned, otherwise BH_HEX_ERR_UNSUPPORTED). block_n, the output rows of one work item
+ * of the decode kernels (16 per wave of a 16-wave workgroup), must be 256; k_split must be 1. */
 typedef struct bh_hex_tile {
   int32_t block_m;
   int32_t block_n;
@@ -144,7 +146,8 @@ int bh_hex_moe_down(const void* act, int32_t act_dtype, int64_t s_am, float* y, 
  * partials need no initial value. Calls that share a workspace must not overlap in time (one
  * stream, or ordered streams). No counterpart in the reference, whose Triton kernels need none:
  * the kernels split an item's inputs between workgroups, and the last workgroup to arrive adds
- * the others' partial sums. */
+ * the others' partial sums. For block_m 128 both sizes are 0 (the prefill kernels need no
+ * workspace; counters and partials may then be null). */
 int bh_hex_moe_workspace(int64_t num_blocks, int64_t n_out, int64_t n_in, int32_t block_m, int32_t glu,
                          int64_t* n_counters, int64_t* n_partials);
 
