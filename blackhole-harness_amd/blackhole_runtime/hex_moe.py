@@ -38,6 +38,10 @@ HEX_BLOCK = 32     # inputs per bit stream (blackhole/anatomy/hex.py:44)
 DIRECT_MAX = int(os.environ.get("BLACKHOLE_HEX_DIRECT_MAX", "32"))      # slots (hex_moe.py:260)
 DEQUANT_MIN = int(os.environ.get("BLACKHOLE_HEX_DEQUANT_MIN", "1024"))  # slots (hex_moe.py:261)
 PREFILL_MIN = 64     # slots per expert above which the fused path takes the 128-slot prefill kernels
+# one launch per layer (plan, gate/up, down, sum) for one tier at 16-slot blocks and few slots;
+# opt-in: on MI355X it measured 91 us per config-2 T=16 layer against 72 us for the four launches
+LAYER = os.environ.get("BLACKHOLE_HEX_LAYER", "0") != "0"
+LAYER_MAX_SLOTS = 512
 
 
 def _n_in(p: dict, bits: int) -> int:
@@ -218,6 +222,53 @@ def _workspace(device: torch.device, block_m: int, num_blocks: int, n_out: int, 
     return cnt, part
 
 
+_LAYER_WORKSPACES: dict = {}
+
+
+def _layer_workspace(device: torch.device, T: int, k: int, H: int, I: int, E: int):
+    """(counters, partials) of the one-launch layer kernel, kept per (device, stream) like
+    _workspace (the kernel leaves its counters at zero)."""
+    lib = _lib.load()
+    nc, npart = _lib.ctypes.c_int64(), _lib.ctypes.c_int64()
+    _lib.check(lib.bh_hex_moe_layer_workspace(T, k, H, I, E, _lib.ctypes.byref(nc), _lib.ctypes.byref(npart)),
+               "bh_hex_moe_layer_workspace")
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    cnt, part = _LAYER_WORKSPACES.get(key, (None, None))
+    keep = not torch.cuda.is_current_stream_capturing()
+    if cnt is None or cnt.numel() < nc.value:
+        cnt = torch.zeros(max(nc.value, 1 << 14), dtype=torch.int32, device=device)
+    if part is None or part.numel() < npart.value:
+        part = torch.empty(max(npart.value, 1 << 16), dtype=torch.float32, device=device)
+    if keep:
+        _LAYER_WORKSPACES[key] = (cnt, part)
+    return cnt, part
+
+
+def layer_wait_flag(device: torch.device | None = None) -> int:
+    """1 if a bounded wait of the layer kernel gave up on this device's current stream since its
+    workspace was made (the output of that call is invalid), else 0. Synchronises."""
+    device = device or torch.device("cuda", torch.cuda.current_device())
+    cnt, _ = _LAYER_WORKSPACES.get((device.index, torch.cuda.current_stream(device).cuda_stream), (None, None))
+    return 0 if cnt is None else int(cnt[32].item())
+
+
+def _launch_layer(x, w, flat_ids, t: HexTier, act, y, out, T: int, k: int) -> bool:
+    """The whole layer in one launch; False when the kernel does not take this shape."""
+    lib = _lib.load()
+    H, I, E = x.shape[1], act.shape[1], t.lookup.numel()
+    ids, code = _ids_arg(flat_ids)
+    cnt, part = _layer_workspace(x.device, T, k, H, I, E)
+    rc = lib.bh_hex_moe_layer(
+        x.data_ptr(), _lib.dtype_code(x.dtype), x.stride(0), ids.data_ptr(), code, w.data_ptr(), T, k,
+        t.struct("gate_proj"), t.struct("up_proj"), t.struct("down_proj"), t.bits, H, I, t.lookup.data_ptr(), E,
+        act.data_ptr(), act.stride(0), y.data_ptr(), y.stride(0), out.data_ptr(), out.stride(0),
+        cnt.data_ptr(), cnt.numel(), part.data_ptr(), part.numel(), _lib.stream_of(x))
+    if rc == _lib.ERR_UNSUPPORTED:
+        return False
+    _lib.check(rc, "bh_hex_moe_layer")
+    return True
+
+
 def _launch_glu(x, act, t: HexTier, sid, eid, npp, S, a_div, bm):
     lib = _lib.load()
     n_out = t.gate_proj["idx"].shape[1]
@@ -284,6 +335,9 @@ def hex_moe_fused(x, topk_weights, topk_ids, tiers: list[HexTier], config: dict 
     c2 = config or default_config(S, H, I, False, E)
     bm1 = _fit_tile(_tile_from(c1), H, I, True)
     bm2 = _fit_tile(_tile_from(c2), I, H, False)
+    if (LAYER and len(tiers) == 1 and bm1 == bm2 == 16 and S <= LAYER_MAX_SLOTS and align_mode == "auto"
+            and _launch_layer(x, w, flat, tiers[0], act, y, out, T, k)):
+        return out
     p1 = plan(flat, E, bm1, align_mode)
     p2 = p1 if bm2 == bm1 else plan(flat, E, bm2, align_mode)
     for t in tiers:

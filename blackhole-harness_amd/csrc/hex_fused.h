@@ -150,6 +150,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
 // Host side.
 int device_cus();
 constexpr int kGemmMt = 8;   // block_m / 16 of the prefill kernels (128-slot blocks)
+// Checks one projection for the fused kernels: scale blocks of 32 or 128 inputs (*sb = B / 32,
+// equal to a nonzero *sb on entry), 16-byte aligned 4-bit rows; clears *words when the scale
+// rows do not allow one load of a unit's scales.
+int proj_setup(const char* who, const bh_hex_proj* w, int bits, int64_t n_in, int* sb, int* words);
 // Launches the prefill kernels for a plan of 128-slot blocks (no workspace).
 int gemm_run(const char* who, bool glu, int bits, int adt, int sb, const MoeArgs& a, int64_t num_blocks,
              hipStream_t stream);
