@@ -30,14 +30,24 @@ __global__ __launch_bounds__(256) void moe_reduce_kernel(const float* __restrict
   const int64_t t = blockIdx.y;
   const int64_t h = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (h >= H) return;
+  // Eight slots at a time, their ids and y rows loaded together (a y row of a slot with an
+  // invalid id is in bounds but unwritten: it is read and dropped); added in slot order.
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int j = 0; j < k; ++j) {
-    const int64_t s = t * k + j;
-    int64_t id;
-    if constexpr (IDT == BH_HEX_I64) id = reinterpret_cast<const int64_t*>(ids)[s];
-    else id = reinterpret_cast<const int32_t*>(ids)[s];
-    if (id < 0 || id >= n_experts) continue;
-    acc += *reinterpret_cast<const f32x4*>(y + s * s_ym + h);
+  for (int j0 = 0; j0 < k; j0 += 8) {
+    int64_t id[8];
+    f32x4 v[8];
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const int64_t s = t * k + j0 + d;
+      if (j0 + d < k) {
+        if constexpr (IDT == BH_HEX_I64) id[d] = reinterpret_cast<const int64_t*>(ids)[s];
+        else id[d] = reinterpret_cast<const int32_t*>(ids)[s];
+        v[d] = *reinterpret_cast<const f32x4*>(y + s * s_ym + h);
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < 8; ++d)
+      if (j0 + d < k && id[d] >= 0 && id[d] < n_experts) acc += v[d];
   }
   if constexpr (ODT == BH_HEX_F32) {
     *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(out) + t * s_ot + h) = acc;
