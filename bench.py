@@ -170,7 +170,7 @@ def kernel_breakdown(cfg, copies, x, w, ids, reps):
     p1 = hm.plan(flat, E, bm1)
     p2 = hm.plan(flat, E, bm2)
     act = torch.empty(S, I, dtype=x.dtype, device=x.device)
-    y = torch.empty(S, H, dtype=torch.float32, device=x.device)
+    y = torch.empty(S, H, dtype=x.dtype if bm2 == 128 else torch.float32, device=x.device)   # as hex_moe_fused
     wf = w.reshape(-1).float().contiguous()
     n_tiers = len(copies[0])
     res = {}

@@ -291,7 +291,7 @@ def _launch_down(act, y, t: HexTier, sid, eid, npp, S, w, bm):
     tile = _lib.HexTile(bm, 256, 1)
     cnt, part = _workspace(act.device, bm, eid.numel(), n_out, n_in, False)
     _lib.check(lib.bh_hex_moe_down(
-        act.data_ptr(), _lib.dtype_code(act.dtype), act.stride(0), y.data_ptr(), y.stride(0),
+        act.data_ptr(), _lib.dtype_code(act.dtype), act.stride(0), y.data_ptr(), _lib.dtype_code(y.dtype), y.stride(0),
         t.struct("down_proj"), t.bits, n_out, n_in,
         sid.data_ptr(), eid.data_ptr(), eid.numel(), npp.data_ptr(), t.lookup.data_ptr(), t.lookup.numel(), S,
         w.data_ptr(), tile, cnt.data_ptr(), cnt.numel(), part.data_ptr(), part.numel(), _lib.stream_of(act)),
@@ -330,11 +330,14 @@ def hex_moe_fused(x, topk_weights, topk_ids, tiers: list[HexTier], config: dict 
     flat = topk_ids.reshape(-1)
     w = topk_weights.reshape(-1).float().contiguous()
     act = torch.empty(S, I, dtype=x.dtype, device=x.device)
-    y = (torch.empty if _covers_all(tiers) else torch.zeros)(S, H, dtype=torch.float32, device=x.device)
     c1 = config or default_config(S, I, H, True, E)
     c2 = config or default_config(S, H, I, False, E)
     bm1 = _fit_tile(_tile_from(c1), H, I, True)
     bm2 = _fit_tile(_tile_from(c2), I, H, False)
+    # y per slot: float32 for the decode kernels; in x.dtype for the prefill kernels, as the
+    # reference's y (hex_moe.py:316), which halves the y traffic of the down kernel and the sum
+    ydt = x.dtype if bm2 == 128 else torch.float32
+    y = (torch.empty if _covers_all(tiers) else torch.zeros)(S, H, dtype=ydt, device=x.device)
     if (LAYER and len(tiers) == 1 and bm1 == bm2 == 16 and S <= LAYER_MAX_SLOTS and align_mode == "auto"
             and _launch_layer(x, w, flat, tiers[0], act, y, out, T, k)):
         return out
@@ -346,8 +349,9 @@ def hex_moe_fused(x, topk_weights, topk_ids, tiers: list[HexTier], config: dict 
         _launch_down(act, y, t, *p2, S, w, bm2)
     ids, code = _ids_arg(flat)
     lib = _lib.load()
-    _lib.check(lib.bh_hex_moe_reduce(y.data_ptr(), y.stride(0), ids.data_ptr(), code, E, T, k, H, out.data_ptr(),
-                                     _lib.dtype_code(out.dtype), out.stride(0), _lib.stream_of(x)), "bh_hex_moe_reduce")
+    _lib.check(lib.bh_hex_moe_reduce(y.data_ptr(), _lib.dtype_code(y.dtype), y.stride(0), ids.data_ptr(), code, E, T, k,
+                                     H, out.data_ptr(), _lib.dtype_code(out.dtype), out.stride(0), _lib.stream_of(x)),
+               "bh_hex_moe_reduce")
     return out
 
 

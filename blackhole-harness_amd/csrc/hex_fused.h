@@ -12,7 +12,7 @@ struct MoeArgs {
   const uint16_t* x;     // activations [rows, K] (bf16/f16 bits)
   int64_t s_xm;
   void* out;             // GLU: act [slots, N] (activation dtype); down: y [slots, N] float
-  int64_t s_om;
+  int64_t s_om;          //   (or, with y16, y in the activation dtype)
   bh_hex_proj w0, w1;    // gate, up (GLU) or down (w0 only)
   const int32_t* sid;
   const int32_t* eid;
@@ -23,6 +23,7 @@ struct MoeArgs {
   int32_t n_experts;
   int32_t a_div;
   int32_t N, K;
+  int32_t y16;           // down: y is in the activation dtype (else float32)
   int32_t scale_words;   // block_scale rows allow one load of a unit's scales (8 or 2 bytes)
                          // (host only: it selects the whole-unit kernel variant)
   float* part;           // workspace: partial sums of items split between workgroups

@@ -317,6 +317,37 @@ __global__ __launch_bounds__(512, 2) void hex_gemm_kernel(MoeArgs a, int n_tiles
         for (int q = 0; q < a.N - col; ++q) dst[q] = st16[row * RS + c + q];
       }
     }
+  } else if (a.y16) {
+    // y in the activation dtype: the whole 128 x 256 tile fills the 64 KB. Column bits 4-5 are
+    // XORed with row bits 2-3 (the four row groups of a write land in distinct banks; 8-half
+    // chunks stay contiguous).
+    uint16_t* const st16 = reinterpret_cast<uint16_t*>(stage);
+    auto at_rc = [](int row, int col) { return row * 256 + (col ^ (((row >> 2) & 3) << 4)); };
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = j * 16 + 4 * lg + r;
+        const float w = slot_w[row];
+#pragma unroll
+        for (int g = 0; g < kNG; ++g)
+          st16[at_rc(row, (wave * kNG + g) * 16 + ln)] = (uint16_t)to_bits<ADT>(acc[j][g][r] * es0 * w);
+      }
+    __syncthreads();
+    // 32 threads per row, 8 outputs (16 bytes) each
+#pragma unroll
+    for (int it = 0; it < kGM * 32 / kGThreads; ++it) {
+      const int row = it * (kGThreads / 32) + tid / 32, c = (tid & 31) * 8;
+      const int slot = slots[row], col = nt * 256 + c;
+      if (slot >= a.num_slots || col >= a.N) continue;
+      uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + (int64_t)slot * a.s_om + col;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(st16 + at_rc(row, c));
+      if (col + 8 <= a.N) {
+        *reinterpret_cast<u32x4*>(dst) = v;
+      } else {
+        for (int q = 0; q < a.N - col; ++q) dst[q] = st16[at_rc(row, c) + q];
+      }
+    }
   } else {
     // 64 rows of 256 floats fill the 64 KB exactly: instead of padding, column bits 4-5 are
     // XORed with row bits 2-3 (conflict-free writes; 4-float chunks stay contiguous)
@@ -390,7 +421,7 @@ int gemm_run(const char* who, bool glu, int bits, int adt, int sb, const MoeArgs
                                                              "4-byte aligned block_scale rows");
   }
   // output rows are written 16 bytes at a time
-  if (a.s_om % (glu ? 8 : 4) || !aligned(a.out, 16))
+  if (a.s_om % ((glu || a.y16) ? 8 : 4) || !aligned(a.out, 16))
     return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": block_m 128 needs 16-byte aligned output rows");
   const int64_t x_rows = cdiv(a.num_slots, a.a_div);
   if (x_rows * a.s_xm * 2 > kOOR) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": activations over 2 GiB");

@@ -23,8 +23,20 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
 
 // ----------------------------------------------------------------------------------- reduction
 
-template <int ODT, int IDT>
-__global__ __launch_bounds__(256) void moe_reduce_kernel(const float* __restrict__ y, int64_t s_ym,
+// Four y values of a slot row as float32 (YDT: F32, BF16 or F16).
+template <int YDT>
+__device__ __forceinline__ f32x4 y4(const void* y, int64_t at) {
+  if constexpr (YDT == BH_HEX_F32) {
+    return *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(y) + at);
+  } else {
+    const u32x2 v = *reinterpret_cast<const u32x2*>(reinterpret_cast<const uint16_t*>(y) + at);
+    return f32x4{from_bits<YDT>(v[0] & 0xFFFFu), from_bits<YDT>(v[0] >> 16), from_bits<YDT>(v[1] & 0xFFFFu),
+                 from_bits<YDT>(v[1] >> 16)};
+  }
+}
+
+template <int ODT, int IDT, int YDT>
+__global__ __launch_bounds__(256) void moe_reduce_kernel(const void* __restrict__ y, int64_t s_ym,
                                                          const void* __restrict__ ids, int32_t n_experts, int32_t k,
                                                          int64_t H, void* __restrict__ out, int64_t s_ot) {
   const int64_t t = blockIdx.y;
@@ -42,7 +54,7 @@ __global__ __launch_bounds__(256) void moe_reduce_kernel(const float* __restrict
       if (j0 + d < k) {
         if constexpr (IDT == BH_HEX_I64) id[d] = reinterpret_cast<const int64_t*>(ids)[s];
         else id[d] = reinterpret_cast<const int32_t*>(ids)[s];
-        v[d] = *reinterpret_cast<const f32x4*>(y + s * s_ym + h);
+        v[d] = y4<YDT>(y, s * s_ym + h);
       }
     }
 #pragma unroll
@@ -231,7 +243,7 @@ extern "C" int bh_hex_moe_glu(const void* x, int32_t x_dtype, int64_t s_xm, void
   return check_launch(who);
 }
 
-extern "C" int bh_hex_moe_down(const void* act, int32_t act_dtype, int64_t s_am, float* y, int64_t s_ym,
+extern "C" int bh_hex_moe_down(const void* act, int32_t act_dtype, int64_t s_am, void* y, int32_t y_dtype, int64_t s_ym,
                                const bh_hex_proj* down, int32_t bits, int64_t n_out, int64_t n_in,
                                const int32_t* sorted_ids, const int32_t* expert_ids, int64_t num_blocks,
                                const int32_t* npp, const int32_t* lookup, int32_t n_experts, int64_t num_slots,
@@ -245,6 +257,8 @@ extern "C" int bh_hex_moe_down(const void* act, int32_t act_dtype, int64_t s_am,
   if (rc) return rc;
   if ((rc = proj_setup(who, down, bits, n_in, &sb, &words))) return rc;
   if (!act || !y || !topk_w) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": null pointer");
+  if (y_dtype != BH_HEX_F32 && y_dtype != act_dtype)
+    return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": y dtype must be F32 or the activation dtype");
   if (s_am % 8 || !aligned(act, 16)) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": act rows must be 16-byte aligned");
   if (num_slots * s_am * 2 > 0x7FFFFFFF) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": act over 2 GiB");
   if (num_blocks == 0 || num_slots == 0) return BH_HEX_OK;
@@ -252,6 +266,7 @@ extern "C" int bh_hex_moe_down(const void* act, int32_t act_dtype, int64_t s_am,
   a.s_xm = s_am;
   a.out = y;
   a.s_om = s_ym;
+  a.y16 = y_dtype != BH_HEX_F32;
   a.w0 = *down;
   a.w1 = *down;
   a.topk_w = topk_w;
@@ -282,29 +297,45 @@ extern "C" int bh_hex_moe_workspace(int64_t num_blocks, int64_t n_out, int64_t n
   return BH_HEX_OK;
 }
 
-extern "C" int bh_hex_moe_reduce(const float* y, int64_t s_ym, const void* topk_ids, int32_t ids_dtype,
+template <int ODT, int IDT>
+static void reduce_ydt(int ydt, dim3 grid, hipStream_t st, const void* y, int64_t s_ym, const void* ids,
+                       int32_t n_experts, int32_t k, int64_t H, void* out, int64_t s_ot) {
+  if (ydt == BH_HEX_F32)
+    hipLaunchKernelGGL((moe_reduce_kernel<ODT, IDT, BH_HEX_F32>), grid, dim3(256), 0, st, y, s_ym, ids, n_experts, k, H,
+                       out, s_ot);
+  else if (ydt == BH_HEX_BF16)
+    hipLaunchKernelGGL((moe_reduce_kernel<ODT, IDT, BH_HEX_BF16>), grid, dim3(256), 0, st, y, s_ym, ids, n_experts, k,
+                       H, out, s_ot);
+  else
+    hipLaunchKernelGGL((moe_reduce_kernel<ODT, IDT, BH_HEX_F16>), grid, dim3(256), 0, st, y, s_ym, ids, n_experts, k, H,
+                       out, s_ot);
+}
+
+extern "C" int bh_hex_moe_reduce(const void* y, int32_t y_dtype, int64_t s_ym, const void* topk_ids, int32_t ids_dtype,
                                  int32_t n_experts, int64_t T, int32_t k, int64_t H, void* out, int32_t out_dtype,
                                  int64_t s_ot, void* stream) {
   const char* who = "bh_hex_moe_reduce";
   if (T < 0 || k <= 0 || H <= 0) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": bad sizes");
+  if (y_dtype != BH_HEX_F32 && y_dtype != BH_HEX_BF16 && y_dtype != BH_HEX_F16)
+    return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": y dtype must be F32, BF16 or F16");
   if (H % 4 || s_ym % 4 || s_ot % 4 || !aligned(y, 16) || !aligned(out, 16))
-    return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": rows must be 16-byte aligned with H % 4 == 0");
+    return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": rows must start at multiples of 4 elements, 16-byte "
+                                                           "aligned, with H % 4 == 0");
   if (ids_dtype != BH_HEX_I32 && ids_dtype != BH_HEX_I64)
     return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": ids dtype must be I32 or I64");
+  if (out_dtype != BH_HEX_F32 && out_dtype != BH_HEX_BF16 && out_dtype != BH_HEX_F16)
+    return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": out dtype must be F32, BF16 or F16");
   if (T == 0) return BH_HEX_OK;
   if (T > 65535) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": more than 65535 tokens");
   const dim3 grid((unsigned)cdiv(H, 1024), (unsigned)T);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-#define BH_RED(ODT, IDT) \
-  hipLaunchKernelGGL((moe_reduce_kernel<ODT, IDT>), grid, dim3(256), 0, st, y, s_ym, topk_ids, n_experts, k, H, out, s_ot)
+#define BH_RED(ODT, IDT) reduce_ydt<ODT, IDT>(y_dtype, grid, st, y, s_ym, topk_ids, n_experts, k, H, out, s_ot)
   if (out_dtype == BH_HEX_F32) {
     if (ids_dtype == BH_HEX_I64) BH_RED(BH_HEX_F32, BH_HEX_I64); else BH_RED(BH_HEX_F32, BH_HEX_I32);
   } else if (out_dtype == BH_HEX_BF16) {
     if (ids_dtype == BH_HEX_I64) BH_RED(BH_HEX_BF16, BH_HEX_I64); else BH_RED(BH_HEX_BF16, BH_HEX_I32);
-  } else if (out_dtype == BH_HEX_F16) {
-    if (ids_dtype == BH_HEX_I64) BH_RED(BH_HEX_F16, BH_HEX_I64); else BH_RED(BH_HEX_F16, BH_HEX_I32);
   } else {
-    return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": out dtype must be F32, BF16 or F16");
+    if (ids_dtype == BH_HEX_I64) BH_RED(BH_HEX_F16, BH_HEX_I64); else BH_RED(BH_HEX_F16, BH_HEX_I32);
   }
 #undef BH_RED
   return check_launch(who);

@@ -463,6 +463,8 @@ __device__ __forceinline__ void moe_range(const MoeArgs& a, MoeSmem<BITS, GLU, M
           const float y = acc[mt][0][r] * es0 * slot_w[row];
           if constexpr (FUSED)
             __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), rout, (int)(at * 4), 0, kCohere);
+          else if (a.y16)
+            reinterpret_cast<uint16_t*>(a.out)[at] = (uint16_t)to_bits<ADT>(y);
           else
             reinterpret_cast<float*>(a.out)[at] = y;
         }

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define BH_HEX_ABI_VERSION 3
+#define BH_HEX_ABI_VERSION 4
 
 enum bh_hex_status {
   BH_HEX_OK = 0,
@@ -129,9 +129,11 @@ int bh_hex_moe_glu(const void* x, int32_t x_dtype, int64_t s_xm, void* act, int6
                    int64_t n_partials, void* stream);
 
 /* The down half over one tier: y[s, o] = (es_d * sum_i act[s, i] W_d[o, i]) * topk_w[s],
- * written as float32 y [num_slots, n_out] (row stride s_ym) for the slots of every block of
- * this tier's experts. Replaces _hex_moe_kernel with GLU=False, MUL_W=True (hex_moe.py:324). */
-int bh_hex_moe_down(const void* act, int32_t act_dtype, int64_t s_am, float* y, int64_t s_ym,
+ * written to y [num_slots, n_out] (row stride s_ym) for the slots of every block of this tier's
+ * experts, in y_dtype: F32, or act_dtype (rounded once per slot, as the reference's y in
+ * x.dtype, hex_moe.py:316). Replaces _hex_moe_kernel with GLU=False, MUL_W=True
+ * (hex_moe.py:324). */
+int bh_hex_moe_down(const void* act, int32_t act_dtype, int64_t s_am, void* y, int32_t y_dtype, int64_t s_ym,
                     const bh_hex_proj* down, int32_t bits, int64_t n_out, int64_t n_in,
                     const int32_t* sorted_ids, const int32_t* expert_ids, int64_t num_blocks, const int32_t* npp,
                     const int32_t* lookup, int32_t n_experts, int64_t num_slots, const float* topk_w,
@@ -152,10 +154,12 @@ int bh_hex_moe_workspace(int64_t num_blocks, int64_t n_out, int64_t n_in, int32_
                          int64_t* n_counters, int64_t* n_partials);
 
 /* out[t, h] = sum_j y[t * k + j, h] over the token's k slots, in float32, rounded once to
- * out_dtype (F32, BF16 or F16); slots whose id (topk_ids, I32 or I64) is outside
- * [0, n_experts) contribute nothing. Replaces y.view(T, k, H).sum(1) (hex_moe.py:325). */
-int bh_hex_moe_reduce(const float* y, int64_t s_ym, const void* topk_ids, int32_t ids_dtype, int32_t n_experts,
-                      int64_t T, int32_t k, int64_t H, void* out, int32_t out_dtype, int64_t s_ot, void* stream);
+ * out_dtype (F32, BF16 or F16); y is F32, BF16 or F16 (y_dtype); slots whose id (topk_ids, I32
+ * or I64) is outside [0, n_experts) contribute nothing. Replaces y.view(T, k, H).sum(1)
+ * (hex_moe.py:325). */
+int bh_hex_moe_reduce(const void* y, int32_t y_dtype, int64_t s_ym, const void* topk_ids, int32_t ids_dtype,
+                      int32_t n_experts, int64_t T, int32_t k, int64_t H, void* out, int32_t out_dtype, int64_t s_ot,
+                      void* stream);
 
 /* A whole decode-regime layer over one tier in one launch: the slot plan, the gate/up half, the
  * down half and the k-slot sum, with the numerics of bh_hex_moe_glu, bh_hex_moe_down and

@@ -102,8 +102,14 @@ def test_host_side_errors():
                                16, 16, 1, 16, 16, 4, 4, 1, ctypes.byref(_lib.HexTile(128, 256, 1)), None, 0, None, 0,
                                None),
             _lib.ERR_UNSUPPORTED, r"n_in % 128")
-    _status(lib.bh_hex_moe_reduce(16, 6, 16, _lib.I64, 4, 2, 2, 6, 16, _lib.BF16, 6, None),
+    _status(lib.bh_hex_moe_reduce(16, _lib.F32, 6, 16, _lib.I64, 4, 2, 2, 6, 16, _lib.BF16, 6, None),
             _lib.ERR_UNSUPPORTED, "H % 4")
+    _status(lib.bh_hex_moe_reduce(16, _lib.I32, 8, 16, _lib.I64, 4, 2, 2, 8, 16, _lib.BF16, 8, None),
+            _lib.ERR_UNSUPPORTED, "y dtype")
+    # y is float32 or the activation dtype
+    _status(lib.bh_hex_moe_down(16, _lib.BF16, 64, 16, _lib.F16, 64, ctypes.byref(w32), 4, 64, 64, 16, 16, 1, 16, 16,
+                                4, 4, 16, ctypes.byref(tile), None, 0, None, 0, None),
+            _lib.ERR_UNSUPPORTED, "y dtype")
 
 
 def test_check_maps_status_to_reference_exceptions():

@@ -305,6 +305,11 @@ def test_down_kernel_exact(bits):
         hm._launch_down(torch.from_numpy(act).to(torch.bfloat16).to(DEV), y, tier, sid, eid, npp, S,
                         torch.from_numpy(tw).to(DEV), bm)
         assert np.array_equal(y.cpu().numpy(), want.astype(np.float32)), bm
+        # y in the activation dtype: the same float32 value, rounded once (to nearest even)
+        y16 = torch.full((S, H), float("nan"), dtype=torch.bfloat16, device=DEV)
+        hm._launch_down(torch.from_numpy(act).to(torch.bfloat16).to(DEV), y16, tier, sid, eid, npp, S,
+                        torch.from_numpy(tw).to(DEV), bm)
+        assert torch.equal(y16.cpu(), torch.from_numpy(want.astype(np.float32)).to(torch.bfloat16)), bm
 
 
 def test_uncovered_experts_contribute_nothing():
