@@ -167,27 +167,29 @@ def kernel_breakdown(cfg, copies, x, w, ids, reps):
     c2 = hm.default_config(S, H, I, False, E)
     bm1 = hm._tile_from(c1)
     bm2 = hm._tile_from(c2)
-    p1 = hm.plan(flat, E, bm1)
-    p2 = hm.plan(flat, E, bm2)
+    n_tiers = len(copies[0])
+    lks = [t.lookup if n_tiers > 1 else None for t in copies[0]]     # per-tier plans, as hex_moe_fused
+    p1 = [hm.plan(flat, E, bm1, "auto", lk) for lk in lks]
+    p2 = [hm.plan(flat, E, bm2, "auto", lk) for lk in lks]
     act = torch.empty(S, I, dtype=x.dtype, device=x.device)
     y = torch.empty(S, H, dtype=x.dtype if bm2 == 128 else torch.float32, device=x.device)   # as hex_moe_fused
     wf = w.reshape(-1).float().contiguous()
-    n_tiers = len(copies[0])
     res = {}
 
     def glu():
         for tiers in copies:
-            for t in tiers:
-                hm._launch_glu(x, act, t, *p1, S, k, bm1)
+            for i, t in enumerate(tiers):
+                hm._launch_glu(x, act, t, *p1[i], S, k, bm1)
 
     def down():
         for tiers in copies:
-            for t in tiers:
-                hm._launch_down(act, y, t, *p2, S, wf, bm2)
+            for i, t in enumerate(tiers):
+                hm._launch_down(act, y, t, *p2[i], S, wf, bm2)
 
     def plan():
         for _ in copies:
-            hm.plan(flat, E, bm1)
+            for lk in lks:
+                hm.plan(flat, E, bm1, "auto", lk)
 
     n = len(copies)
     res["glu_us"] = event_time_ms(graph_of(glu), reps) * 1e3 / (n * n_tiers)

@@ -51,6 +51,7 @@ SIGNATURES = {
     "bh_hex_route_topk": (ctypes.c_int, [_P, _I32, _I64, _I64, _I32, _I32, _I32, _P, _P, _I32, _P]),
     "bh_hex_align_max_blocks": (ctypes.c_int64, [_I64, _I32, _I32]),
     "bh_hex_align": (ctypes.c_int, [_P, _I32, _I64, _I32, _I32, _P, _P, _P, _P]),
+    "bh_hex_align_tier": (ctypes.c_int, [_P, _I32, _I64, _I32, _P, _I32, _P, _P, _P, _P]),
     "bh_hex_direct": (ctypes.c_int, [_P, _I32, _I64, _I32, _P, _P, _P, _P]),
     "bh_hex_moe_glu": (ctypes.c_int, [_P, _I32, _I64, _P, _I64, _PROJ, _PROJ, _I32, _I64, _I64, _P, _P, _I64, _P,
                                       _P, _I32, _I64, _I32, _TILE, _P, _I64, _P, _I64, _P]),
@@ -65,7 +66,7 @@ SIGNATURES = {
                                                   ctypes.POINTER(ctypes.c_int64)]),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lib = None
 

@@ -118,10 +118,12 @@ def _ids_arg(ids: torch.Tensor) -> tuple[torch.Tensor, int]:
     return ids, _lib.dtype_code(ids.dtype)
 
 
-def align(ids: torch.Tensor, n: int, block_m: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+def align(ids: torch.Tensor, n: int, block_m: int, lookup: torch.Tensor | None = None
+          ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Group slots by expert, each expert's run padded to block_m, without a host sync
     (hex_moe.py:201-222): sorted slot ids int32 [B * block_m] (S = padding), the expert of every
-    block int32 [B] (-1 = unused), the padded length int32 [1]; B = ceil(S/block_m) + min(n, S)."""
+    block int32 [B] (-1 = unused), the padded length int32 [1]; B = ceil(S/block_m) + min(n, S).
+    With a tier's lookup (int32 [n]) only that tier's slots are placed (bh_hex_align_tier)."""
     lib = _lib.load()
     _lib.require_gpu(ids)
     ids, code = _ids_arg(ids)
@@ -133,8 +135,15 @@ def align(ids: torch.Tensor, n: int, block_m: int) -> tuple[torch.Tensor, torch.
     sid = torch.empty(nb * block_m, dtype=torch.int32, device=dev)
     eid = torch.empty(nb, dtype=torch.int32, device=dev)
     npp = torch.empty(1, dtype=torch.int32, device=dev)
-    _lib.check(lib.bh_hex_align(ids.data_ptr(), code, S, n, block_m, sid.data_ptr(), eid.data_ptr(), npp.data_ptr(),
-                                _lib.stream_of(ids)), "bh_hex_align")
+    if lookup is None:
+        _lib.check(lib.bh_hex_align(ids.data_ptr(), code, S, n, block_m, sid.data_ptr(), eid.data_ptr(),
+                                    npp.data_ptr(), _lib.stream_of(ids)), "bh_hex_align")
+    else:
+        if lookup.dtype != torch.int32 or lookup.numel() != n or lookup.device != ids.device:
+            raise ValueError(f"lookup must be int32 [{n}] on {ids.device}")
+        _lib.check(lib.bh_hex_align_tier(ids.data_ptr(), code, S, n, lookup.contiguous().data_ptr(), block_m,
+                                         sid.data_ptr(), eid.data_ptr(), npp.data_ptr(), _lib.stream_of(ids)),
+                   "bh_hex_align_tier")
     return sid, eid, npp
 
 
@@ -153,15 +162,17 @@ def direct(ids: torch.Tensor, block_m: int) -> tuple[torch.Tensor, torch.Tensor,
     return sid, eid, npp
 
 
-def plan(ids: torch.Tensor, n: int, block_m: int, mode: str = "auto"):
+def plan(ids: torch.Tensor, n: int, block_m: int, mode: str = "auto", lookup: torch.Tensor | None = None):
     """(sorted slot ids, block experts, padded length) for the fused kernels (hex_moe.py:248-257):
     direct for at most DIRECT_MAX slots (or mode="direct"), else the align kernel. The reference's
-    "vllm" and "torch" modes name other sorts with the same outputs; both map to the align kernel."""
+    "vllm" and "torch" modes name other sorts with the same outputs; both map to the align kernel.
+    A tier's lookup restricts an aligned plan to that tier's slots (direct plans ignore it: the
+    kernels skip other tiers' blocks)."""
     if mode not in ("auto", "direct", "vllm", "torch"):
         raise ValueError(f"unknown plan mode {mode!r}")
     if mode == "direct" or (mode == "auto" and ids.numel() <= DIRECT_MAX):
         return direct(ids, block_m)
-    return align(ids, n, block_m)
+    return align(ids, n, block_m, lookup)
 
 
 # --------------------------------------------------------------------------- tiles
@@ -341,11 +352,15 @@ def hex_moe_fused(x, topk_weights, topk_ids, tiers: list[HexTier], config: dict 
     if (LAYER and len(tiers) == 1 and bm1 == bm2 == 16 and S <= LAYER_MAX_SLOTS and align_mode == "auto"
             and _launch_layer(x, w, flat, tiers[0], act, y, out, T, k)):
         return out
-    p1 = plan(flat, E, bm1, align_mode)
-    p2 = p1 if bm2 == bm1 else plan(flat, E, bm2, align_mode)
+    # one plan per tier when there are several, so each tier's launches walk only its own blocks
+    plans = []
     for t in tiers:
+        lk = t.lookup if len(tiers) > 1 else None
+        p1 = plan(flat, E, bm1, align_mode, lk)
+        plans.append((p1, p1 if bm2 == bm1 else plan(flat, E, bm2, align_mode, lk)))
+    for t, (p1, _) in zip(tiers, plans):
         _launch_glu(x, act, t, *p1, S, k, bm1)
-    for t in tiers:
+    for t, (_, p2) in zip(tiers, plans):
         _launch_down(act, y, t, *p2, S, w, bm2)
     ids, code = _ids_arg(flat)
     lib = _lib.load()

@@ -113,6 +113,14 @@ __device__ __forceinline__ int64_t load_id(const void* p, int64_t i) {
   else return reinterpret_cast<const int32_t*>(p)[i];
 }
 
+// The expert slot i is placed under, or -1: ids outside [0, n) are not placed, nor, with a tier
+// lookup, experts the tier does not hold (lookup < 0).
+template <int IDT>
+__device__ __forceinline__ int64_t placed_id(const void* p, int64_t i, int32_t n, const int32_t* lookup) {
+  const int64_t e = load_id<IDT>(p, i);
+  return (e >= 0 && e < n && (!lookup || lookup[e] >= 0)) ? e : -1;
+}
+
 // Inclusive prefix sum over the workgroup of one value per thread (1024 threads).
 __device__ int block_incl_scan(int v, int* wsum) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -158,7 +166,8 @@ __device__ __forceinline__ uint64_t match_key(int key, int nbits) {
 // are then placed by align_scatter_kernel, one workgroup per 1024 slots.
 template <int IDT, bool SCATTER>
 __global__ __launch_bounds__(kAlignThreads) void align_kernel(const void* __restrict__ ids, int64_t S, int32_t n,
-                                                              int32_t bm, int64_t max_blocks,
+                                                              const int32_t* __restrict__ lookup, int32_t bm,
+                                                              int64_t max_blocks,
                                                               int32_t* __restrict__ sorted_ids,
                                                               int32_t* __restrict__ expert_ids,
                                                               int32_t* __restrict__ npp) {
@@ -179,7 +188,7 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(const void* __rest
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
       const int64_t i = c0 + k * kWave + lane;
-      const int64_t e = i < r1 ? load_id<IDT>(ids, i) : -1;
+      const int64_t e = i < r1 ? placed_id<IDT>(ids, i, n, lookup) : -1;
       key[k] = (e >= 0 && e < n) ? (int)e : n;
     }
   };
@@ -217,7 +226,7 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(const void* __rest
 #pragma unroll
       for (int k = 0; k < kBatch; ++k) {
         const int64_t i = b0 + k * kAlignThreads + tid;
-        e[k] = i < S ? load_id<IDT>(ids, i) : -1;
+        e[k] = i < S ? placed_id<IDT>(ids, i, n, lookup) : -1;
       }
 #pragma unroll
       for (int k = 0; k < kBatch; ++k)
@@ -278,7 +287,8 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(const void* __rest
 // (counted again here), in slot order (per wave by ballot rank, then over the waves).
 template <int IDT>
 __global__ __launch_bounds__(kAlignThreads) void align_scatter_kernel(const void* __restrict__ ids, int64_t S,
-                                                                      int32_t n, int32_t bm, int64_t max_blocks,
+                                                                      int32_t n, const int32_t* __restrict__ lookup,
+                                                                      int32_t bm, int64_t max_blocks,
                                                                       int32_t* __restrict__ sorted_ids,
                                                                       const int32_t* __restrict__ expert_ids,
                                                                       const int32_t* __restrict__ npp) {
@@ -299,7 +309,7 @@ __global__ __launch_bounds__(kAlignThreads) void align_scatter_kernel(const void
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
       const int64_t i = b0 + k * kAlignThreads + tid;
-      e[k] = i < c0 ? load_id<IDT>(ids, i) : -1;
+      e[k] = i < c0 ? placed_id<IDT>(ids, i, n, lookup) : -1;
     }
 #pragma unroll
     for (int k = 0; k < kBatch; ++k)
@@ -313,8 +323,8 @@ __global__ __launch_bounds__(kAlignThreads) void align_scatter_kernel(const void
   const int64_t i = c0 + tid;
   int key = n;
   if (i < S) {
-    const int64_t e = load_id<IDT>(ids, i);
-    if (e >= 0 && e < n) key = (int)e;
+    const int64_t e = placed_id<IDT>(ids, i, n, lookup);
+    if (e >= 0) key = (int)e;
   }
   const uint64_t same = match_key(key, nbits);
   const int rank = __popcll(same & below);
@@ -385,38 +395,54 @@ extern "C" int64_t bh_hex_align_max_blocks(int64_t S, int32_t n_experts, int32_t
   return cdiv(S, block_m) + (S < n_experts ? S : (int64_t)n_experts);
 }
 
-extern "C" int bh_hex_align(const void* ids, int32_t ids_dtype, int64_t S, int32_t n_experts, int32_t block_m,
-                            int32_t* sorted_ids, int32_t* expert_ids, int32_t* npp, void* stream) {
-  if (block_m <= 0) return fail(BH_HEX_ERR_VALUE, "bh_hex_align: block_m must be positive");
+static int align_run(const char* who, const void* ids, int32_t ids_dtype, int64_t S, int32_t n_experts,
+                     const int32_t* lookup, int32_t block_m, int32_t* sorted_ids, int32_t* expert_ids, int32_t* npp,
+                     void* stream) {
+  const std::string w(who);
+  if (block_m <= 0) return fail(BH_HEX_ERR_VALUE, w + ": block_m must be positive");
   if (n_experts <= 0 || n_experts > kAlignMaxExperts)
-    return fail(BH_HEX_ERR_UNSUPPORTED, "bh_hex_align: experts must be in 1.." + std::to_string(kAlignMaxExperts));
-  if (S < 0 || S > (int64_t)INT32_MAX / 2) return fail(BH_HEX_ERR_VALUE, "bh_hex_align: slot count out of range");
+    return fail(BH_HEX_ERR_UNSUPPORTED, w + ": experts must be in 1.." + std::to_string(kAlignMaxExperts));
+  if (S < 0 || S > (int64_t)INT32_MAX / 2) return fail(BH_HEX_ERR_VALUE, w + ": slot count out of range");
   if (ids_dtype != BH_HEX_I32 && ids_dtype != BH_HEX_I64)
-    return fail(BH_HEX_ERR_UNSUPPORTED, "bh_hex_align: ids dtype must be I32 or I64");
-  if (!npp || (S > 0 && (!ids || !sorted_ids || !expert_ids))) return fail(BH_HEX_ERR_VALUE, "bh_hex_align: null pointer");
+    return fail(BH_HEX_ERR_UNSUPPORTED, w + ": ids dtype must be I32 or I64");
+  if (!npp || (S > 0 && (!ids || !sorted_ids || !expert_ids))) return fail(BH_HEX_ERR_VALUE, w + ": null pointer");
   const int64_t max_blocks = bh_hex_align_max_blocks(S, n_experts, block_m);
-  if (max_blocks * block_m > (int64_t)INT32_MAX) return fail(BH_HEX_ERR_VALUE, "bh_hex_align: plan too large");
+  if (max_blocks * block_m > (int64_t)INT32_MAX) return fail(BH_HEX_ERR_VALUE, w + ": plan too large");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   // up to kAlignSplit slots one workgroup does everything; above, it writes the block plan and
   // one workgroup per 1024 slots places them
   const bool split = S > kAlignSplit;
   const dim3 chunks((unsigned)cdiv(S, kAlignThreads));
-#define BH_ALIGN(IDT)                                                                                              \
-  do {                                                                                                             \
-    if (split) {                                                                                                   \
-      hipLaunchKernelGGL((align_kernel<IDT, false>), dim3(1), dim3(kAlignThreads), 0, st, ids, S, n_experts, block_m, \
-                         max_blocks, sorted_ids, expert_ids, npp);                                                 \
-      hipLaunchKernelGGL((align_scatter_kernel<IDT>), chunks, dim3(kAlignThreads), 0, st, ids, S, n_experts, block_m, \
-                         max_blocks, sorted_ids, expert_ids, npp);                                                 \
-    } else {                                                                                                       \
-      hipLaunchKernelGGL((align_kernel<IDT, true>), dim3(1), dim3(kAlignThreads), 0, st, ids, S, n_experts, block_m,  \
-                         max_blocks, sorted_ids, expert_ids, npp);                                                 \
-    }                                                                                                              \
+  const dim3 one(1), threads(kAlignThreads);
+#define BH_ALIGN(IDT)                                                                                             \
+  do {                                                                                                            \
+    if (split) {                                                                                                  \
+      hipLaunchKernelGGL((align_kernel<IDT, false>), one, threads, 0, st, ids, S, n_experts, lookup, block_m,     \
+                         max_blocks, sorted_ids, expert_ids, npp);                                                \
+      hipLaunchKernelGGL((align_scatter_kernel<IDT>), chunks, threads, 0, st, ids, S, n_experts, lookup, block_m, \
+                         max_blocks, sorted_ids, expert_ids, npp);                                                \
+    } else {                                                                                                      \
+      hipLaunchKernelGGL((align_kernel<IDT, true>), one, threads, 0, st, ids, S, n_experts, lookup, block_m,      \
+                         max_blocks, sorted_ids, expert_ids, npp);                                                \
+    }                                                                                                             \
   } while (0)
   if (ids_dtype == BH_HEX_I64) BH_ALIGN(BH_HEX_I64);
   else BH_ALIGN(BH_HEX_I32);
 #undef BH_ALIGN
-  return check_launch("bh_hex_align");
+  return check_launch(who);
+}
+
+extern "C" int bh_hex_align(const void* ids, int32_t ids_dtype, int64_t S, int32_t n_experts, int32_t block_m,
+                            int32_t* sorted_ids, int32_t* expert_ids, int32_t* npp, void* stream) {
+  return align_run("bh_hex_align", ids, ids_dtype, S, n_experts, nullptr, block_m, sorted_ids, expert_ids, npp, stream);
+}
+
+extern "C" int bh_hex_align_tier(const void* ids, int32_t ids_dtype, int64_t S, int32_t n_experts,
+                                 const int32_t* lookup, int32_t block_m, int32_t* sorted_ids, int32_t* expert_ids,
+                                 int32_t* npp, void* stream) {
+  if (!lookup) return fail(BH_HEX_ERR_VALUE, "bh_hex_align_tier: null lookup");
+  return align_run("bh_hex_align_tier", ids, ids_dtype, S, n_experts, lookup, block_m, sorted_ids, expert_ids, npp,
+                   stream);
 }
 
 extern "C" int bh_hex_direct(const void* ids, int32_t ids_dtype, int64_t S, int32_t block_m, int32_t* sorted_ids,

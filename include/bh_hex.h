@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define BH_HEX_ABI_VERSION 4
+#define BH_HEX_ABI_VERSION 5
 
 enum bh_hex_status {
   BH_HEX_OK = 0,
@@ -107,6 +107,14 @@ int64_t bh_hex_align_max_blocks(int64_t S, int32_t n_experts, int32_t block_m);
  * ids (I32 or I64) outside [0, n_experts) are not placed. */
 int bh_hex_align(const void* ids, int32_t ids_dtype, int64_t S, int32_t n_experts, int32_t block_m,
                  int32_t* sorted_ids, int32_t* expert_ids, int32_t* npp, void* stream);
+
+/* bh_hex_align over the slots of one tier: slots whose expert has no entry in the tier's lookup
+ * (lookup[e] < 0; int32 [n_experts], as HexTier.prepare builds it) are not placed either, so the
+ * plan holds only this tier's blocks. Same outputs and max_blocks otherwise. With several tiers
+ * the fused launches of a tier then walk only its own blocks. No counterpart in the reference,
+ * which shares one plan between its tiers (hex_moe.py:318-324). */
+int bh_hex_align_tier(const void* ids, int32_t ids_dtype, int64_t S, int32_t n_experts, const int32_t* lookup,
+                      int32_t block_m, int32_t* sorted_ids, int32_t* expert_ids, int32_t* npp, void* stream);
 
 /* One block per slot, no sorting (hex_moe.py:228-237, direct): sorted_ids[s * block_m] = s and S
  * elsewhere, expert_ids = ids as int32, npp = S * block_m. */

@@ -124,6 +124,31 @@ def test_align_bit_exact(S, n, bm, skew, idt):
         assert np.array_equal(g.cpu().numpy(), w)
 
 
+@pytest.mark.parametrize("S,n,bm", [(128, 96, 16), (2048, 96, 32), (9000, 96, 128), (40000, 128, 64), (50, 8, 16)])
+def test_align_tier_bit_exact(S, n, bm):
+    """A tier's plan places only the slots of experts it holds: the oracle's align of that subset
+    of slots, its positions mapped back to the original slot numbers, padded to the full plan's
+    length (S as padding, -1 past the last block). Both align paths (one workgroup up to 4096
+    slots, plan + placement above)."""
+    say(f"align_tier S={S} n={n} bm={bm}")
+    rng = np.random.default_rng(S + bm)
+    ids = rng.integers(0, n, S)
+    lookup = np.full(n, -1, np.int32)
+    held = rng.permutation(n)[: n // 2]
+    lookup[held] = np.arange(held.size)
+    sub = np.nonzero(lookup[ids] >= 0)[0]
+    s_sub, e_sub, npp_sub = O.align(ids[sub], n, bm)
+    mb = -(-S // bm) + min(n, S)
+    want_sid = np.full(mb * bm, S, np.int32)
+    want_sid[: s_sub.size] = np.where(s_sub < sub.size, sub[np.minimum(s_sub, max(sub.size - 1, 0))], S)
+    want_eid = np.full(mb, -1, np.int32)
+    want_eid[: e_sub.size] = e_sub
+    sid, eid, npp = hm.align(torch.from_numpy(ids).to(DEV), n, bm, torch.from_numpy(lookup).to(DEV))
+    assert np.array_equal(sid.cpu().numpy(), want_sid)
+    assert np.array_equal(eid.cpu().numpy(), want_eid)
+    assert npp.item() == int(npp_sub[0])
+
+
 def test_align_reference_example():
     say("align reference example")
     ids = torch.tensor([2, 0, 0, 2, 2, 1, 3, 0], device=DEV)
