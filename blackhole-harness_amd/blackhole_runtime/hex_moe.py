@@ -189,20 +189,22 @@ def _tile_from(cfg: dict) -> int:
 
 def _fit_tile(bm: int, n_in: int, n_out: int, glu: bool) -> int:
     """The prefill kernels (block_m 128) step through the inputs 128 at a time and write output
-    rows (act in the activation dtype, y in float32) 16 bytes at a time; other widths take the
-    64-slot decode kernels."""
-    return 64 if bm == 128 and (n_in % 128 or n_out % (8 if glu else 4)) else bm
+    rows (act and y, both in the activation dtype) 16 bytes at a time; other widths take the
+    32-slot decode kernels."""
+    return 32 if bm == 128 and (n_in % 128 or n_out % 8) else bm
 
 
 def default_config(slots: int, n_out: int, n_in: int, glu: bool, n_experts: int = 0) -> dict:
     """Tile choice by slot count (hex_moe.py:264-283), or BLACKHOLE_HEX_TILES="BM". BLOCK_M grows
-    with the slots each expert gets, so an expert's weights are streamed by few blocks."""
+    with the slots each expert gets, so an expert's weights are streamed by few blocks. 64-slot
+    blocks are never chosen by default: on MI355X their gate/up kernel spills registers and ran
+    over twice as long as 32-slot blocks on config 4's batch."""
     env = os.environ.get("BLACKHOLE_HEX_TILES")
     if env:
         bm = _tile_from({"BLOCK_M": int(env.split(",")[0])})
     else:
         per_expert = slots / max(1, n_experts or slots)
-        bm = 16 if per_expert <= 16 else (32 if per_expert <= 48 else (64 if per_expert <= PREFILL_MIN else 128))
+        bm = 16 if per_expert <= 16 else (32 if per_expert <= PREFILL_MIN else 128)
     return {"BLOCK_M": _fit_tile(bm, n_in, n_out, glu), "BLOCK_N": 256}
 
 

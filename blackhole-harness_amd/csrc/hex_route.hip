@@ -113,12 +113,14 @@ __device__ __forceinline__ int64_t load_id(const void* p, int64_t i) {
   else return reinterpret_cast<const int32_t*>(p)[i];
 }
 
-// The expert slot i is placed under, or -1: ids outside [0, n) are not placed, nor, with a tier
-// lookup, experts the tier does not hold (lookup < 0).
-template <int IDT>
+// The expert slot i is placed under, or -1: ids outside [0, n) are not placed, nor, for a tier's
+// plan (TIER), experts the tier does not hold (lookup < 0). (A template flag, not a null test:
+// the plain plan's batched id loads then compile without the dependent lookup load.)
+template <int IDT, bool TIER>
 __device__ __forceinline__ int64_t placed_id(const void* p, int64_t i, int32_t n, const int32_t* lookup) {
   const int64_t e = load_id<IDT>(p, i);
-  return (e >= 0 && e < n && (!lookup || lookup[e] >= 0)) ? e : -1;
+  if constexpr (TIER) return (e >= 0 && e < n && lookup[e] >= 0) ? e : -1;
+  else return (e >= 0 && e < n) ? e : -1;
 }
 
 // Inclusive prefix sum over the workgroup of one value per thread (1024 threads).
@@ -164,7 +166,7 @@ __device__ __forceinline__ uint64_t match_key(int key, int nbits) {
 // each wave then places its own range in order with no further workgroup barrier.
 // Without SCATTER the workgroup only counts (LDS atomics) and writes the block plan; the slots
 // are then placed by align_scatter_kernel, one workgroup per 1024 slots.
-template <int IDT, bool SCATTER>
+template <int IDT, bool SCATTER, bool TIER>
 __global__ __launch_bounds__(kAlignThreads) void align_kernel(const void* __restrict__ ids, int64_t S, int32_t n,
                                                               const int32_t* __restrict__ lookup, int32_t bm,
                                                               int64_t max_blocks,
@@ -188,7 +190,7 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(const void* __rest
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
       const int64_t i = c0 + k * kWave + lane;
-      const int64_t e = i < r1 ? placed_id<IDT>(ids, i, n, lookup) : -1;
+      const int64_t e = i < r1 ? placed_id<IDT, TIER>(ids, i, n, lookup) : -1;
       key[k] = (e >= 0 && e < n) ? (int)e : n;
     }
   };
@@ -226,7 +228,7 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(const void* __rest
 #pragma unroll
       for (int k = 0; k < kBatch; ++k) {
         const int64_t i = b0 + k * kAlignThreads + tid;
-        e[k] = i < S ? placed_id<IDT>(ids, i, n, lookup) : -1;
+        e[k] = i < S ? placed_id<IDT, TIER>(ids, i, n, lookup) : -1;
       }
 #pragma unroll
       for (int k = 0; k < kBatch; ++k)
@@ -285,7 +287,7 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(const void* __rest
 // Places the slots of chunk blockIdx.x (1024 slots) after align_kernel<IDT, false> wrote the
 // block plan: the chunk's slots of each expert go after the expert's slots in earlier chunks
 // (counted again here), in slot order (per wave by ballot rank, then over the waves).
-template <int IDT>
+template <int IDT, bool TIER>
 __global__ __launch_bounds__(kAlignThreads) void align_scatter_kernel(const void* __restrict__ ids, int64_t S,
                                                                       int32_t n, const int32_t* __restrict__ lookup,
                                                                       int32_t bm, int64_t max_blocks,
@@ -309,7 +311,7 @@ __global__ __launch_bounds__(kAlignThreads) void align_scatter_kernel(const void
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
       const int64_t i = b0 + k * kAlignThreads + tid;
-      e[k] = i < c0 ? placed_id<IDT>(ids, i, n, lookup) : -1;
+      e[k] = i < c0 ? placed_id<IDT, TIER>(ids, i, n, lookup) : -1;
     }
 #pragma unroll
     for (int k = 0; k < kBatch; ++k)
@@ -323,7 +325,7 @@ __global__ __launch_bounds__(kAlignThreads) void align_scatter_kernel(const void
   const int64_t i = c0 + tid;
   int key = n;
   if (i < S) {
-    const int64_t e = placed_id<IDT>(ids, i, n, lookup);
+    const int64_t e = placed_id<IDT, TIER>(ids, i, n, lookup);
     if (e >= 0) key = (int)e;
   }
   const uint64_t same = match_key(key, nbits);
@@ -414,20 +416,25 @@ static int align_run(const char* who, const void* ids, int32_t ids_dtype, int64_
   const bool split = S > kAlignSplit;
   const dim3 chunks((unsigned)cdiv(S, kAlignThreads));
   const dim3 one(1), threads(kAlignThreads);
-#define BH_ALIGN(IDT)                                                                                             \
+#define BH_ALIGN(IDT, TIER)                                                                                       \
   do {                                                                                                            \
     if (split) {                                                                                                  \
-      hipLaunchKernelGGL((align_kernel<IDT, false>), one, threads, 0, st, ids, S, n_experts, lookup, block_m,     \
-                         max_blocks, sorted_ids, expert_ids, npp);                                                \
-      hipLaunchKernelGGL((align_scatter_kernel<IDT>), chunks, threads, 0, st, ids, S, n_experts, lookup, block_m, \
-                         max_blocks, sorted_ids, expert_ids, npp);                                                \
+      hipLaunchKernelGGL((align_kernel<IDT, false, TIER>), one, threads, 0, st, ids, S, n_experts, lookup,        \
+                         block_m, max_blocks, sorted_ids, expert_ids, npp);                                       \
+      hipLaunchKernelGGL((align_scatter_kernel<IDT, TIER>), chunks, threads, 0, st, ids, S, n_experts, lookup,    \
+                         block_m, max_blocks, sorted_ids, expert_ids, npp);                                       \
     } else {                                                                                                      \
-      hipLaunchKernelGGL((align_kernel<IDT, true>), one, threads, 0, st, ids, S, n_experts, lookup, block_m,      \
+      hipLaunchKernelGGL((align_kernel<IDT, true, TIER>), one, threads, 0, st, ids, S, n_experts, lookup, block_m, \
                          max_blocks, sorted_ids, expert_ids, npp);                                                \
     }                                                                                                             \
   } while (0)
-  if (ids_dtype == BH_HEX_I64) BH_ALIGN(BH_HEX_I64);
-  else BH_ALIGN(BH_HEX_I32);
+  if (lookup) {
+    if (ids_dtype == BH_HEX_I64) BH_ALIGN(BH_HEX_I64, true);
+    else BH_ALIGN(BH_HEX_I32, true);
+  } else {
+    if (ids_dtype == BH_HEX_I64) BH_ALIGN(BH_HEX_I64, false);
+    else BH_ALIGN(BH_HEX_I32, false);
+  }
 #undef BH_ALIGN
   return check_launch(who);
 }

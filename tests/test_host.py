@@ -55,9 +55,9 @@ def test_default_config_and_env(monkeypatch):
     assert hm.default_config(8, 768, 2048, True, 96) == {"BLOCK_M": 16, "BLOCK_N": 256}    # T=1 decode
     assert hm.default_config(128, 768, 2048, True, 96)["BLOCK_M"] == 16                    # T=16
     assert hm.default_config(32768, 2048, 768, False, 96)["BLOCK_M"] == 128                # prefill
-    assert hm.default_config(32768, 2048, 96, False, 96)["BLOCK_M"] == 64                  # inputs % 128 != 0
+    assert hm.default_config(32768, 2048, 96, False, 96)["BLOCK_M"] == 32                  # inputs % 128 != 0
     assert hm.default_config(3000, 768, 2048, True, 96)["BLOCK_M"] == 32
-    assert hm.default_config(6000, 768, 2048, True, 96)["BLOCK_M"] == 64
+    assert hm.default_config(6000, 768, 2048, True, 96)["BLOCK_M"] == 32                   # (64 never by default)
     monkeypatch.setenv("BLACKHOLE_HEX_TILES", "64")
     assert hm.default_config(8, 768, 2048, True, 96) == {"BLOCK_M": 64, "BLOCK_N": 256}
     # the reference's own config keys map onto the tile
@@ -65,8 +65,9 @@ def test_default_config_and_env(monkeypatch):
     assert hm._tile_from({"BLOCK_M": 64, "BLOCK_N": 128}) == 64
     assert hm._tile_from({"BLOCK_M": 128, "BLOCK_N": 128}) == 128
     assert hm._tile_from({"BLOCK_M": 24}) == 32
-    assert hm._fit_tile(128, 768, 2048, False) == 128 and hm._fit_tile(128, 160, 2048, False) == 64
-    assert hm._fit_tile(128, 2048, 100, True) == 64 and hm._fit_tile(128, 2048, 100, False) == 128
+    assert hm._fit_tile(128, 768, 2048, False) == 128 and hm._fit_tile(128, 160, 2048, False) == 32
+    assert hm._fit_tile(128, 2048, 100, True) == 32 and hm._fit_tile(128, 2048, 100, False) == 32
+    assert hm._fit_tile(128, 2048, 104, False) == 128 and hm._fit_tile(64, 2048, 100, False) == 64
     assert hm._fit_tile(32, 160, 99, True) == 32
 
 
