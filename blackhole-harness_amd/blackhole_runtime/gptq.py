@@ -1,0 +1,159 @@
+"""HEX producer with GPTQ rounding onto each expert's level table (torch; GPU or CPU tensors).
+
+The parts the pipeline's hexvllm stage writes for a stack of expert matrices
+(harness/blackhole_pipeline/stages/hexvllm.py:75-96, hex_parts), from the weights W [n, out, in]
+and each expert's input Hessian H [n, in, in] (the sum of x x^T over the tokens routed to it):
+
+  header     expert scale es = max|W| / 448; per 32-input block an fp8 e4m3 scale of the block's
+             max|w| / es, rounded to nearest even (reaper/gpu_perf/headers.py:43-55)
+  levels     L sorted levels per expert: Lloyd k-means on the block-normalised weights, started
+             at quantiles, each value weighted by its input channel's Hessian diagonal times its
+             block scale squared (error in weight units), 20 rounds, a seeded sample of 2^17
+             values when there are more (headers.py:66-83, 96-103)
+  rounding   GPTQ (Frantar et al. 2022) onto the table: columns in order, each rounded to the
+             nearest level of its scaled table, its error spread over the later columns through
+             the upper Cholesky factor of H^-1, with lazy updates per 128 columns; dead columns
+             (zero weights or no activation) stay zero; the damping grows until both Cholesky
+             factorisations succeed (reaper/gpu_perf/gptq.py:36-83, 134-141)
+  packing    table indices, fp8 block codes and the HEX bit stream
+             (harness/blackhole_pipeline/pack.py:53-86, 104-110)
+
+The arithmetic (float32 sweeps, float64 factorisations, the order of every reduction on the
+CPU) follows those files so that, on CPU tensors, the parts equal the reference's bit for bit;
+on the GPU the k-means sums run as atomics and float32 division is not correctly rounded, so
+scales and levels can differ in the last bits and a code can flip where a value sits within
+rounding of a midpoint.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .quant import FP8_MAX, HEX_BLOCK, pack
+
+
+def block_headers(W: torch.Tensor, block: int = HEX_BLOCK):
+    """(block-normalised values [n, out, in/block, block] in [-1, 1], dequant block scales
+    [n, out, in/block, 1], expert scales [n]) of W [n, out, in] (in a multiple of block)."""
+    n, out, inp = W.shape
+    if inp % block:
+        raise ValueError(f"input width {inp} is not a multiple of the block {block}")
+    x = W.float().view(n, out, inp // block, block)
+    amax = x.abs().amax(-1, keepdim=True)
+    es = (amax.amax(dim=(1, 2, 3), keepdim=True) / FP8_MAX).clamp(min=1e-30)
+    blk = (amax / es).clamp(max=FP8_MAX).to(torch.float8_e4m3fn).float() * es
+    blk = torch.where(blk > 0, blk, torch.ones_like(blk))
+    return (x / blk).clamp(-1, 1), blk, es.reshape(n)
+
+
+def fit_levels(xn: torch.Tensor, wt: torch.Tensor | None, L: int, iters: int = 20, sample: int = 1 << 17,
+               seed: int = 0) -> torch.Tensor:
+    """Sorted levels [n, L]: weighted 1-D Lloyd k-means per row of xn [n, N] (weights wt [n, N]),
+    started at the L inner quantiles; a seeded sample of `sample` columns when N is larger (the
+    draw comes from a CPU generator, so it is the same on every device)."""
+    n, N = xn.shape
+    if N > sample:
+        g = torch.Generator(device="cpu").manual_seed(seed)
+        pick = torch.randint(0, N, (sample,), generator=g).to(xn.device)
+        xn = xn[:, pick]
+        wt = wt[:, pick] if wt is not None else None
+    w = wt if wt is not None else torch.ones_like(xn)
+    q = torch.linspace(0, 1, L + 2, device=xn.device)[1:-1]
+    lev = torch.quantile(xn.float(), q, dim=1).T.contiguous()
+    for _ in range(iters):
+        mids = (lev[:, 1:] + lev[:, :-1]) / 2
+        a = torch.searchsorted(mids.contiguous(), xn.contiguous())
+        num = torch.zeros(n, L, device=xn.device).scatter_add_(1, a, xn * w)
+        den = torch.zeros(n, L, device=xn.device).scatter_add_(1, a, w)
+        lev = torch.where(den > 0, num / den.clamp(min=1e-30), lev)
+        lev = lev.sort(1).values
+    return lev
+
+
+def nearest_index(x: torch.Tensor, levels: torch.Tensor) -> torch.Tensor:
+    """Index of the nearest of each row's sorted levels [n, L] for x [n, ...] (midpoint search)."""
+    n = x.shape[0]
+    mids = (levels[:, 1:] + levels[:, :-1]) / 2
+    return torch.searchsorted(mids.contiguous(), x.reshape(n, -1).contiguous()).view(x.shape)
+
+
+def hessian_factor(W: torch.Tensor, H: torch.Tensor, damp: float = 0.01):
+    """(W with dead columns zeroed, float32 upper Cholesky factor of the damped H^-1 [n, in, in],
+    dead columns [n, in]). An expert with an all-zero Hessian is rounded plainly (H = I); a column
+    is dead when its weights are all zero or its channel is never active. The damping, a
+    fraction of the mean live diagonal, triples for a problem until both factorisations succeed."""
+    W = W.float().clone()
+    H = H.double().clone()
+    n, _, m = W.shape
+    eye = torch.eye(m, dtype=H.dtype, device=H.device)
+    H[(H.diagonal(dim1=1, dim2=2) == 0).all(1)] = eye
+    dead = (H.diagonal(dim1=1, dim2=2) == 0) | (W.abs().amax(1) == 0)
+    live = (~dead).to(H.dtype)
+    H = H * live[:, :, None] * live[:, None, :] + eye * dead.to(H.dtype)[:, :, None]
+    W = W * (~dead)[:, None, :]
+    diag = H.diagonal(dim1=1, dim2=2)
+    base = (diag * live).sum(1) / live.sum(1).clamp(min=1)
+    base = torch.where(base > 0, base, torch.ones_like(base))
+    d = torch.full((n,), damp, dtype=H.dtype, device=H.device)
+    for _ in range(6):
+        Lc, info = torch.linalg.cholesky_ex(H + (d * base)[:, None, None] * eye)
+        U, info2 = torch.linalg.cholesky_ex(torch.cholesky_inverse(Lc), upper=True)
+        bad = (info != 0) | (info2 != 0) | ~torch.isfinite(U).all(-1).all(-1)
+        if not bad.any():
+            return W, U.float(), dead
+        d = torch.where(bad, d * 3, d)
+    raise RuntimeError("GPTQ: Hessian not positive definite even with heavy damping")
+
+
+def gptq_sweep(W: torch.Tensor, U: torch.Tensor, round_col, block: int = 128) -> torch.Tensor:
+    """The GPTQ column sweep over W [n, out, in] with the factor U [n, in, in]: column c is rounded
+    by round_col(values [n, out, 1], c), its error divided by U[c, c] is pushed onto the rest of its
+    128-column block at once and onto the later blocks when the block ends. Returns Q."""
+    m = W.shape[-1]
+    Q = torch.zeros_like(W)
+    for b0 in range(0, m, block):
+        b1 = min(b0 + block, m)
+        Wb = W[..., b0:b1].clone()
+        Eb = torch.zeros_like(Wb)
+        Ub = U[:, b0:b1, b0:b1]
+        for j in range(b1 - b0):
+            q = round_col(Wb[..., j:j + 1], b0 + j)
+            Q[..., b0 + j:b0 + j + 1] = q
+            e = (Wb[..., j:j + 1] - q) / Ub[:, j, j][:, None, None]
+            Wb[..., j:] -= e @ Ub[:, j:j + 1, j:]
+            Eb[..., j:j + 1] = e
+        W[..., b1:] -= Eb @ U[:, b0:b1, b1:]
+    return Q
+
+
+@torch.no_grad()
+def quantize_experts_gptq(W: torch.Tensor, H: torch.Tensor, L: int = 16, block: int = HEX_BLOCK,
+                          damp: float = 0.01, sweep_block: int = 128) -> dict:
+    """HEX parts of W [n, out, in] with GPTQ rounding under the Hessians H [n, in, in]:
+    {"idx" int32 [n, out, in/32*bits], "block_scale" uint8 [n, out, in/block], "expert_scale"
+    float32 [n], "levels" float32 [n, L], "q" float32 [n, out, in] (the rounded weights)}."""
+    if W.dim() != 3 or H.dim() != 3 or H.shape != (W.shape[0], W.shape[2], W.shape[2]):
+        raise ValueError(f"W [n, out, in] and H [n, in, in] expected, got {tuple(W.shape)} and {tuple(H.shape)}")
+    bits = int(L).bit_length() - 1
+    if L != 1 << bits or bits not in (3, 4):
+        raise ValueError("HEX tables have 8 or 16 levels")
+    if block % HEX_BLOCK:
+        raise ValueError(f"the scale block must be a multiple of {HEX_BLOCK}")
+    n, out, inp = W.shape
+    xn, blk, es = block_headers(W, block)
+    cw = H.diagonal(dim1=-2, dim2=-1).float().view(n, 1, inp // block, block)
+    wt = (cw.expand(n, out, -1, -1) * blk.pow(2)).reshape(n, -1)
+    levels = fit_levels(xn.reshape(n, -1), wt, L).contiguous().float()
+    scale = blk.expand(-1, -1, -1, block).reshape(n, out, inp)        # per-element dequant scale
+
+    def round_col(x: torch.Tensor, c: int) -> torch.Tensor:
+        s = scale[..., c:c + 1]
+        return torch.gather(levels, 1, nearest_index((x / s).clamp(-1, 1), levels).reshape(n, -1)).view(x.shape) * s
+
+    Wd, U, dead = hessian_factor(W, H, damp)
+    Q = gptq_sweep(Wd, U, round_col, sweep_block) * (~dead)[:, None, :]
+    codes = nearest_index((Q / scale).clamp(-1, 1), levels)
+    es_w = (W.float().abs().amax(dim=(1, 2)) / FP8_MAX).clamp(min=1e-30)
+    bs = (blk[..., 0] / es_w[:, None, None]).clamp(max=FP8_MAX).to(torch.float8_e4m3fn).view(torch.uint8)
+    return {"idx": pack(codes, bits), "block_scale": bs.contiguous(), "expert_scale": es_w.float().contiguous(),
+            "levels": levels, "q": Q}
