@@ -22,7 +22,9 @@ The arithmetic (float32 sweeps, float64 factorisations, the order of every reduc
 CPU) follows those files so that, on CPU tensors, the parts equal the reference's bit for bit;
 on the GPU the k-means sums run as atomics and float32 division is not correctly rounded, so
 scales and levels can differ in the last bits and a code can flip where a value sits within
-rounding of a midpoint.
+rounding of a midpoint. The GPU's batched float64 Cholesky has returned wrong factors with a
+success code here, so every device factorisation is checked by its residual and the failing
+problems are factorised again on the CPU.
 """
 
 from __future__ import annotations
@@ -77,6 +79,41 @@ def nearest_index(x: torch.Tensor, levels: torch.Tensor) -> torch.Tensor:
     return torch.searchsorted(mids.contiguous(), x.reshape(n, -1).contiguous()).view(x.shape)
 
 
+def _checked(A: torch.Tensor, F: torch.Tensor, info: torch.Tensor, residual, redo):
+    """On a GPU, replace the factors of problems whose residual(F) against A exceeds 1e-9 of
+    max|A| by redo(A on the CPU): the device's batched float64 Cholesky has returned wrong factors
+    with a zero info code on this platform."""
+    if A.device.type == "cpu":
+        return F, info
+    bad = (info == 0) & (residual(F) > 1e-9 * A.abs().amax(dim=(-2, -1)))
+    if bad.any():
+        Fc, ic = redo(A[bad].cpu())
+        F[bad] = Fc.to(F.device)
+        info[bad] = ic.to(info.device)
+    return F, info
+
+
+def _cholesky(A: torch.Tensor, upper: bool = False):
+    """Batched float64 Cholesky factor (lower, or upper) with per-problem info, checked by
+    max|F F^T - A| (or F^T F) on a GPU."""
+    F, info = torch.linalg.cholesky_ex(A, upper=upper)
+    mt = lambda x: x.transpose(-1, -2)                                            # noqa: E731
+    res = (lambda F_: (mt(F_) @ F_ - A).abs().amax(dim=(-2, -1))) if upper else \
+        (lambda F_: (F_ @ mt(F_) - A).abs().amax(dim=(-2, -1)))
+    return _checked(A, F, info, res, lambda a: torch.linalg.cholesky_ex(a, upper=upper))
+
+
+def _inverse_from_factor(L: torch.Tensor, A: torch.Tensor) -> torch.Tensor:
+    """A^-1 from its lower factor L, checked by max|A^-1 A - I| on a GPU."""
+    Ci = torch.cholesky_inverse(L)
+    eye = torch.eye(A.shape[-1], dtype=A.dtype, device=A.device)
+    Ci, _ = _checked(A, Ci, torch.zeros(A.shape[0], dtype=torch.int32, device=A.device),
+                     lambda C: (C @ A - eye).abs().amax(dim=(-2, -1)) * A.abs().amax(dim=(-2, -1)),
+                     lambda a: (torch.cholesky_inverse(torch.linalg.cholesky_ex(a)[0]),
+                                torch.zeros(a.shape[0], dtype=torch.int32)))
+    return Ci
+
+
 def hessian_factor(W: torch.Tensor, H: torch.Tensor, damp: float = 0.01):
     """(W with dead columns zeroed, float32 upper Cholesky factor of the damped H^-1 [n, in, in],
     dead columns [n, in]). An expert with an all-zero Hessian is rounded plainly (H = I); a column
@@ -96,8 +133,9 @@ def hessian_factor(W: torch.Tensor, H: torch.Tensor, damp: float = 0.01):
     base = torch.where(base > 0, base, torch.ones_like(base))
     d = torch.full((n,), damp, dtype=H.dtype, device=H.device)
     for _ in range(6):
-        Lc, info = torch.linalg.cholesky_ex(H + (d * base)[:, None, None] * eye)
-        U, info2 = torch.linalg.cholesky_ex(torch.cholesky_inverse(Lc), upper=True)
+        Hd = H + (d * base)[:, None, None] * eye
+        Lc, info = _cholesky(Hd)
+        U, info2 = _cholesky(_inverse_from_factor(Lc, Hd), upper=True)
         bad = (info != 0) | (info2 != 0) | ~torch.isfinite(U).all(-1).all(-1)
         if not bad.any():
             return W, U.float(), dead

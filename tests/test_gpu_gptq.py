@@ -72,3 +72,53 @@ def test_gptq_config2_width_and_fused_kernels():
     # the parts are HEX parts: the dequant kernel gives back Q
     deq = hm.hex_dequant(got["idx"], got["block_scale"], got["expert_scale"], got["levels"], 4, "R")
     torch.testing.assert_close(deq, got["q"], rtol=2e-6, atol=0)
+
+
+def test_gptq_tiers_through_the_folder_checker(tmp_path):
+    """Producer to consumer: a two-layer model's experts GPTQ-quantized on the GPU into a 16-level
+    and an 8-level tier, written as a blackhole-hex folder, pass the folder checker's kernel check
+    (the fused kernels against the float32 reference MoE on those tiers)."""
+    say("gptq tiers through the folder checker")
+    import json
+
+    from safetensors.torch import save_file
+
+    from blackhole_runtime import check_folder as cf
+    E, H, I, hot = 6, 256, 128, 3
+    g = torch.Generator().manual_seed(11)
+    t = {}
+    for li in range(2):
+        pre = f"model.layers.{li}.mlp.experts"
+        for L, ids in ((16, list(range(hot))), (8, list(range(hot, E)))):
+            t[f"{pre}.tier{L}.experts"] = torch.tensor(ids, dtype=torch.int32)
+            for proj, (o, i) in (("gate_proj", (I, H)), ("up_proj", (I, H)), ("down_proj", (H, I))):
+                W = (torch.randn(len(ids), o, i, generator=g) * 0.02).to(DEV)
+                X = torch.randn(len(ids), 512, i, generator=g).to(DEV)
+                parts = gptq.quantize_experts_gptq(W, X.transpose(1, 2).contiguous() @ X, L)
+                for part in ("idx", "block_scale", "expert_scale", "levels"):
+                    t[f"{pre}.tier{L}.{proj}.{part}"] = parts[part].cpu().contiguous()
+    save_file(t, str(tmp_path / "model.safetensors"))
+    (tmp_path / "config.json").write_text(json.dumps({
+        "text_config": {"num_experts": E, "num_experts_per_tok": 2, "hidden_size": H, "moe_intermediate_size": I},
+        "quantization_config": {"quant_method": "blackhole-hex"}}))
+    r = cf.check(tmp_path, DEV, tokens=9)
+    say(f"  {r}")
+    assert r["ok"] and r["checked"] == 2 and r["kernel_rel"] < 1e-2, r
+
+
+def test_wrong_device_factor_is_recomputed():
+    """A factor that does not reproduce its matrix (as the device routine has returned with a zero
+    info code) is replaced by the CPU's; correct ones are kept."""
+    say("gptq: checked Cholesky")
+    g = torch.Generator().manual_seed(3)
+    X = torch.randn(3, 300, 64, generator=g, dtype=torch.float64)
+    A = (X.transpose(1, 2).contiguous() @ X).to(DEV)
+    L, info = torch.linalg.cholesky_ex(A)
+    L = L.clone()
+    L[1] += 0.5                                              # a wrong factor with info 0
+    mt = lambda x: x.transpose(-1, -2)                       # noqa: E731
+    F, info = gptq._checked(A, L, info, lambda F_: (F_ @ mt(F_) - A).abs().amax(dim=(-2, -1)),
+                            lambda a: torch.linalg.cholesky_ex(a))
+    want = torch.linalg.cholesky(A.cpu())
+    torch.testing.assert_close(F.cpu(), want, rtol=1e-10, atol=1e-10)
+    assert info.tolist() == [0, 0, 0]
