@@ -425,7 +425,7 @@ def main(argv=None) -> int:
         torch.cuda.empty_cache()
         keys = ("ms_per_step", "tokens_per_s", "mfma_frac", "hbm_gbps", "hbm_frac", "unique_experts")
         # the other configs: (config, resident copies, token batches, timed calls per batch)
-        for c, n_copies, batches, steps in ((3, 2, (4096,), 16), (4, 4, (256,), 100), (5, 8, (16, 2048), 32)):
+        for c, n_copies, batches, steps in ((3, 2, (4096,), 16), (4, 4, (256,), 100), (5, 8, (1, 16, 256, 2048, 8192), 32)):
             layers = build_tiers(CONFIGS[c], a.block, n_copies, dev)
             for Ts in batches:
                 r, _ = run_layer(CONFIGS[c], layers, Ts, steps, a.warmup, a.block, breakdown=False)
