@@ -243,10 +243,13 @@ __global__ __launch_bounds__(512, 2) void hex_gemm_kernel(MoeArgs a, int n_tiles
       for (int j = 0; j < 8; ++j) {
         __builtin_amdgcn_sched_barrier(0);
         if (j + 1 < 8) afrag(j + 1, hq, av[(j + 1) & 1]);
-        // the next step's loads: words in the first half step, tile chunks in the second
+        // the next step's loads: tile chunks in the first half step (they must land in LDS by
+        // the step's closing barrier, so they get the longer lead), words in the second (their
+        // registers are waited for only where the next step reads them). Measured against the
+        // opposite order: 3% (gate/up) and 4.5% (down) less time at a 4096-token prefill.
         const int t = hq * 8 + j;
-        if (t < kNG) load_w1(sw, t, ws[1 - P][t], ss[1 - P][t]);
-        else if (t >= 8 && t < 8 + kChunks) load_a1(sa, t - 8, an);
+        if (t < kChunks) load_a1(sa, t, an);
+        else if (t >= 8 && t < 8 + kNG) load_w1(sw, t - 8, ws[1 - P][t - 8], ss[1 - P][t - 8]);
         __builtin_amdgcn_sched_barrier(0);
         const u32x4 (&x)[2] = av[j & 1];
         if constexpr (SB == 4) {

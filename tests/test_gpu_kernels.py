@@ -258,6 +258,32 @@ def test_prefill_kernels(dt, block):
     assert hm.default_config(1200, I, H, True, E)["BLOCK_M"] == 128
 
 
+@pytest.mark.parametrize("bits", [3, 4])
+def test_prefill_scale_extremes(bits):
+    """The 128-slot kernels with one scale per 128 inputs keep each accumulator in units of the
+    current block's scale. Zero scales (in a row's first block, its last block, or every
+    block), the smallest subnormal scale (0x01) next to the largest (0x7E = 448), and 0x7F
+    (480) must all give the oracle's layer. (bf16 only: with 448 and 480 scales the intermediate
+    activations pass f16's 65504, and the float32 oracle's f16 rounding of them overflows too.)"""
+    say(f"prefill scale extremes bits={bits}")
+    E, H, I, k = 4, 512, 256, 2
+    ref, tiers = make_layer(E, H, I, 0, (bits,), seed=41, block=128)
+    for t_ref, t in zip(ref, tiers):
+        for proj in ("gate_proj", "up_proj", "down_proj"):
+            bs = t_ref[proj]["block_scale"]            # [n, out, in / 128]
+            nb = bs.shape[2]
+            bs[:, 0::5, 0] = 0x00                      # first block zero
+            bs[:, 1::5, nb - 1] = 0x80                 # last block -0
+            bs[:, 2::13, :] = 0x00                     # the whole row zero
+            bs[:, 3::5, 0::2] = 0x01                   # 2^-9 next to 448
+            bs[:, 3::5, 1::2] = 0x7E
+            bs[:, 4::7, nb // 2] = 0x7F
+            getattr(t, proj)["block_scale"].copy_(torch.from_numpy(bs))
+    for T in (300, 129):
+        err = run_fused(ref, tiers, T, E, k, H, seed=T, config={"BLOCK_M": 128})
+        assert err < TOL_16, (T, err)
+
+
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("bits", [3, 4])
 def test_quantized_layer(dt, bits):
