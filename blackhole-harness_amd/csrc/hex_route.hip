@@ -184,36 +184,38 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(const void* __rest
   // whole 64-slot chunks per wave (a small batch leaves the later waves empty)
   const int64_t per = ((S + kAlignWaves - 1) / kAlignWaves + kWave - 1) / kWave * kWave;
   const int64_t r0 = min(S, (int64_t)w * per), r1 = min(S, r0 + per);
-  // the keys of kBatch chunks of 64 slots from c0, loaded together (their loads overlap)
-  constexpr int kBatch = 16;
-  auto keys = [&](int64_t c0, int (&key)[kBatch]) {
-#pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-      const int64_t i = c0 + k * kWave + lane;
-      const int64_t e = i < r1 ? placed_id<IDT, TIER>(ids, i, n, lookup) : -1;
-      key[k] = (e >= 0 && e < n) ? (int)e : n;
-    }
-  };
+  constexpr int kBatch = 16;                 // id loads issued together by the counting loop
   auto match = [&](int key) { return match_key(key, nbits); };
 
+  // With SCATTER (at most kAlignSplit slots) a wave's range is at most kSC chunks of 64, so its
+  // keys and their lane matches are kept in registers from the count to the placement (one
+  // round trip to the ids), and only the waves that hold slots (nw) enter the offset pass.
+  constexpr int kSC = (int)(kAlignSplit / kAlignThreads);
+  int skey[kSC];
+  uint64_t ssame[kSC];
+  const int nw = per ? (int)((S + per - 1) / per) : 0;
   if constexpr (SCATTER) {
-    for (int e = lane; e < n; e += kWave) wcnt[w][e] = 0;
-    __builtin_amdgcn_wave_barrier();
-    for (int64_t c0 = r0; c0 < r1; c0 += kBatch * kWave) {
-      int key[kBatch];
-      keys(c0, key);
+    if (r0 < r1) {
+      for (int e = lane; e < n; e += kWave) wcnt[w][e] = 0;
 #pragma unroll
-      for (int k = 0; k < kBatch; ++k) {
-        if (c0 + k * kWave >= r1) break;                 // (uniform: the wave's range ends)
-        const uint64_t same = match(key[k]);
-        if (key[k] < n && __popcll(same & below) == 0) wcnt[w][key[k]] += __popcll(same);
+      for (int k = 0; k < kSC; ++k) {
+        const int64_t i = r0 + k * kWave + lane;
+        const int64_t e = i < r1 ? placed_id<IDT, TIER>(ids, i, n, lookup) : -1;
+        skey[k] = (e >= 0 && e < n) ? (int)e : n;
+      }
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int k = 0; k < kSC; ++k) {
+        if (r0 + k * kWave >= r1) break;                 // (uniform: the wave's range ends)
+        ssame[k] = match(skey[k]);
+        if (skey[k] < n && __popcll(ssame[k] & below) == 0) wcnt[w][skey[k]] += __popcll(ssame[k]);
         __builtin_amdgcn_wave_barrier();
       }
     }
     __syncthreads();
     for (int e = tid; e < n; e += kAlignThreads) {        // counts -> offsets over the waves
       int acc = 0;
-      for (int v = 0; v < kAlignWaves; ++v) {
+      for (int v = 0; v < nw; ++v) {
         const int c = wcnt[v][e];
         wcnt[v][e] = acc;
         acc += c;
@@ -264,23 +266,18 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(const void* __rest
   // each wave places its range, chunk by chunk in slot order: a lane's row is its expert's
   // run start + the wave's offset in that run + its rank among the chunk's lanes of the expert;
   // the key's lowest lane then moves the wave's offset on (after every lane has read it)
-  for (int64_t c0 = r0; c0 < r1; c0 += kBatch * kWave) {
-    int key[kBatch];
-    keys(c0, key);
 #pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-      if (c0 + k * kWave >= r1) break;                   // (uniform: the wave's range ends)
-      const int64_t i = c0 + k * kWave + lane;
-      const uint64_t same = match(key[k]);
-      const int rank = __popcll(same & below);
-      if (key[k] < n) {
-        const int64_t pos = (int64_t)start[key[k]] + wcnt[w][key[k]] + rank;
-        if (pos < max_blocks * bm) sorted_ids[pos] = (int32_t)i;
-      }
-      __builtin_amdgcn_wave_barrier();
-      if (key[k] < n && rank == 0) wcnt[w][key[k]] += __popcll(same);
-      __builtin_amdgcn_wave_barrier();
+  for (int k = 0; k < kSC; ++k) {
+    if (r0 + k * kWave >= r1) break;                     // (uniform: the wave's range ends)
+    const int64_t i = r0 + k * kWave + lane;
+    const int rank = __popcll(ssame[k] & below);
+    if (skey[k] < n) {
+      const int64_t pos = (int64_t)start[skey[k]] + wcnt[w][skey[k]] + rank;
+      if (pos < max_blocks * bm) sorted_ids[pos] = (int32_t)i;
     }
+    __builtin_amdgcn_wave_barrier();
+    if (skey[k] < n && rank == 0) wcnt[w][skey[k]] += __popcll(ssame[k]);
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
