@@ -236,6 +236,16 @@ def _workspace(device: torch.device, block_m: int, num_blocks: int, n_out: int, 
 
 
 _LAYER_WORKSPACES: dict = {}
+_SIDE_STREAMS: dict = {}
+
+
+def _side_stream(device: torch.device) -> torch.cuda.Stream:
+    """The second stream of a device (default priority) that runs the launches of a layer's
+    second and later tiers."""
+    s = _SIDE_STREAMS.get(device.index)
+    if s is None:
+        s = _SIDE_STREAMS[device.index] = torch.cuda.Stream(device)
+    return s
 
 
 def _layer_workspace(device: torch.device, T: int, k: int, H: int, I: int, E: int):
@@ -354,16 +364,28 @@ def hex_moe_fused(x, topk_weights, topk_ids, tiers: list[HexTier], config: dict 
     if (LAYER and len(tiers) == 1 and bm1 == bm2 == 16 and S <= LAYER_MAX_SLOTS and align_mode == "auto"
             and _launch_layer(x, w, flat, tiers[0], act, y, out, T, k)):
         return out
-    # one plan per tier when there are several, so each tier's launches walk only its own blocks
-    plans = []
-    for t in tiers:
-        lk = t.lookup if len(tiers) > 1 else None
+    def run_tier(t: HexTier, lk: torch.Tensor | None) -> None:
+        # one plan per tier when there are several, so each tier's launches walk only its blocks
         p1 = plan(flat, E, bm1, align_mode, lk)
-        plans.append((p1, p1 if bm2 == bm1 else plan(flat, E, bm2, align_mode, lk)))
-    for t, (p1, _) in zip(tiers, plans):
+        p2 = p1 if bm2 == bm1 else plan(flat, E, bm2, align_mode, lk)
         _launch_glu(x, act, t, *p1, S, k, bm1)
-    for t, (_, p2) in zip(tiers, plans):
         _launch_down(act, y, t, *p2, S, w, bm2)
+
+    if len(tiers) == 1:
+        run_tier(tiers[0], None)
+    else:
+        # Each slot is served by one tier, so the tiers write disjoint rows of act and y: the
+        # later tiers run on a side stream beside the first (each stream keeps its own
+        # workspace), which overlaps one tier's ramp and tail with the other's streaming. The
+        # caller's stream waits for the side stream before the k-slot sum.
+        main = torch.cuda.current_stream(x.device)
+        side = _side_stream(x.device)
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            for t in tiers[1:]:
+                run_tier(t, t.lookup)
+        run_tier(tiers[0], tiers[0].lookup)
+        main.wait_stream(side)
     ids, code = _ids_arg(flat)
     lib = _lib.load()
     _lib.check(lib.bh_hex_moe_reduce(y.data_ptr(), _lib.dtype_code(y.dtype), y.stride(0), ids.data_ptr(), code, E, T, k,
