@@ -384,14 +384,19 @@ def test_width_mismatch_and_dtype_errors():
         hm.hex_moe_fused(torch.zeros(2, H, device=DEV), w, ids, tiers)
 
 
-@pytest.mark.parametrize("bm", [None, 128])
-def test_graph_capture_replays_match_eager(bm):
+@pytest.mark.parametrize("bm,split", [(None, 8), (128, 8), (128, 0)])
+def test_graph_capture_replays_match_eager(bm, split):
     """The fused path captured in a hipGraph: several replays, with eager work between them,
-    each equal to the eager result (default tiles, and the 128-slot prefill kernels)."""
-    say(f"graph capture bm={bm}")
+    each equal to the eager result (default tiles, and the 128-slot prefill kernels). Two tiers
+    (the second on the side stream), or one tier (with the prefill kernels, its two halves by
+    expert on the two streams)."""
+    say(f"graph capture bm={bm} split={split}")
     E, H, I, k, T = 16, 256, 128, 4, 8 if bm is None else 300
     cfg = None if bm is None else {"BLOCK_M": bm}
-    ref, tiers = make_layer(E, H, I, 8, (4, 3), seed=12)
+    ref, tiers = make_layer(E, H, I, split, (4, 3), seed=12)
+    if bm == 128 and split == 0:
+        assert len(tiers) == 1 and tiers[0]._halves and hm.SPLIT
+        assert run_fused(ref, tiers, T, E, k, H, seed=5, config=cfg) < TOL_16
     w, ids = routing(T, E, k, seed=5)
     x = torch.randn(T, H, generator=torch.Generator().manual_seed(0)).to(torch.bfloat16).to(DEV)
     wd, idd = torch.from_numpy(w).to(DEV), torch.from_numpy(ids).to(DEV)
@@ -433,12 +438,14 @@ def run_layer(tier, x, w, ids):
 
 
 def per_projection(tiers, x, w, ids):
-    old = hm.LAYER
+    """The four launches over each whole tier (no split into expert halves), as the one-launch
+    layer kernel runs them."""
+    old = hm.LAYER, hm.SPLIT
     try:
-        hm.LAYER = False
+        hm.LAYER, hm.SPLIT = False, False
         return hm.hex_moe_fused(x, w, ids, tiers)
     finally:
-        hm.LAYER = old
+        hm.LAYER, hm.SPLIT = old
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
