@@ -52,6 +52,8 @@ SIGNATURES = {
     "bh_hex_align_max_blocks": (ctypes.c_int64, [_I64, _I32, _I32]),
     "bh_hex_align": (ctypes.c_int, [_P, _I32, _I64, _I32, _I32, _P, _P, _P, _P]),
     "bh_hex_align_tier": (ctypes.c_int, [_P, _I32, _I64, _I32, _P, _I32, _P, _P, _P, _P]),
+    "bh_hex_align_workspace": (ctypes.c_int64, [_I64, _I32]),
+    "bh_hex_align_ws": (ctypes.c_int, [_P, _I32, _I64, _I32, _P, _I32, _P, _I64, _P, _P, _P, _P]),
     "bh_hex_direct": (ctypes.c_int, [_P, _I32, _I64, _I32, _P, _P, _P, _P]),
     "bh_hex_moe_glu": (ctypes.c_int, [_P, _I32, _I64, _P, _I64, _PROJ, _PROJ, _I32, _I64, _I64, _P, _P, _I64, _P,
                                       _P, _I32, _I64, _I32, _TILE, _P, _I64, _P, _I64, _P]),
@@ -66,7 +68,7 @@ SIGNATURES = {
                                                   ctypes.POINTER(ctypes.c_int64)]),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lib = None
 

@@ -134,12 +134,14 @@ def _ids_arg(ids: torch.Tensor) -> tuple[torch.Tensor, int]:
     return ids, _lib.dtype_code(ids.dtype)
 
 
-def align(ids: torch.Tensor, n: int, block_m: int, lookup: torch.Tensor | None = None
+def align(ids: torch.Tensor, n: int, block_m: int, lookup: torch.Tensor | None = None, _chunked: bool = True
           ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Group slots by expert, each expert's run padded to block_m, without a host sync
     (hex_moe.py:201-222): sorted slot ids int32 [B * block_m] (S = padding), the expert of every
     block int32 [B] (-1 = unused), the padded length int32 [1]; B = ceil(S/block_m) + min(n, S).
-    With a tier's lookup (int32 [n]) only that tier's slots are placed (bh_hex_align_tier)."""
+    With a tier's lookup (int32 [n]) only that tier's slots are placed (bh_hex_align_tier).
+    Above 4096 slots the slots are counted per 1024-slot chunk into a workspace
+    (bh_hex_align_ws); _chunked=False takes the entry points without one."""
     lib = _lib.load()
     _lib.require_gpu(ids)
     ids, code = _ids_arg(ids)
@@ -151,12 +153,18 @@ def align(ids: torch.Tensor, n: int, block_m: int, lookup: torch.Tensor | None =
     sid = torch.empty(nb * block_m, dtype=torch.int32, device=dev)
     eid = torch.empty(nb, dtype=torch.int32, device=dev)
     npp = torch.empty(1, dtype=torch.int32, device=dev)
-    if lookup is None:
+    if lookup is not None and (lookup.dtype != torch.int32 or lookup.numel() != n or lookup.device != ids.device):
+        raise ValueError(f"lookup must be int32 [{n}] on {ids.device}")
+    nws = lib.bh_hex_align_workspace(S, n)
+    if _chunked and nws > 0:
+        ws = torch.empty(nws, dtype=torch.int32, device=dev)
+        lk = None if lookup is None else lookup.contiguous().data_ptr()
+        _lib.check(lib.bh_hex_align_ws(ids.data_ptr(), code, S, n, lk, block_m, ws.data_ptr(), nws, sid.data_ptr(),
+                                       eid.data_ptr(), npp.data_ptr(), _lib.stream_of(ids)), "bh_hex_align_ws")
+    elif lookup is None:
         _lib.check(lib.bh_hex_align(ids.data_ptr(), code, S, n, block_m, sid.data_ptr(), eid.data_ptr(),
                                     npp.data_ptr(), _lib.stream_of(ids)), "bh_hex_align")
     else:
-        if lookup.dtype != torch.int32 or lookup.numel() != n or lookup.device != ids.device:
-            raise ValueError(f"lookup must be int32 [{n}] on {ids.device}")
         _lib.check(lib.bh_hex_align_tier(ids.data_ptr(), code, S, n, lookup.contiguous().data_ptr(), block_m,
                                          sid.data_ptr(), eid.data_ptr(), npp.data_ptr(), _lib.stream_of(ids)),
                    "bh_hex_align_tier")

@@ -172,7 +172,7 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(const void* __rest
                                                               int64_t max_blocks,
                                                               int32_t* __restrict__ sorted_ids,
                                                               int32_t* __restrict__ expert_ids,
-                                                              int32_t* __restrict__ npp) {
+                                                              int32_t* __restrict__ npp, int32_t* __restrict__ ws) {
   __shared__ int cnt[kAlignMaxExperts];      // slots per expert
   __shared__ int start[kAlignMaxExperts];    // first padded row of the expert's run
   __shared__ int wcnt[kAlignWaves][kAlignMaxExperts];   // per wave: count, then offset in the run
@@ -219,6 +219,25 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(const void* __rest
         const int c = wcnt[v][e];
         wcnt[v][e] = acc;
         acc += c;
+      }
+      cnt[e] = acc;
+    }
+  } else if (ws) {
+    // align_count_kernel's counts per 1024-slot chunk -> each chunk's exclusive prefix per
+    // expert (in place, read by align_scatter_kernel) and the totals
+    const int nch = (int)((S + kAlignThreads - 1) / kAlignThreads);
+    for (int e = tid; e < n; e += kAlignThreads) {
+      int acc = 0;
+      for (int c0 = 0; c0 < nch; c0 += 8) {
+        int v[8];
+#pragma unroll
+        for (int d = 0; d < 8; ++d) v[d] = c0 + d < nch ? ws[(int64_t)(c0 + d) * n + e] : 0;
+#pragma unroll
+        for (int d = 0; d < 8; ++d)
+          if (c0 + d < nch) {
+            ws[(int64_t)(c0 + d) * n + e] = acc;
+            acc += v[d];
+          }
       }
       cnt[e] = acc;
     }
@@ -281,16 +300,37 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(const void* __rest
   }
 }
 
+// Counts the placed slots of chunk blockIdx.x (1024 slots) per expert into ws[chunk * n + e]
+// (every entry of the chunk's row is written, so the workspace needs no clearing).
+template <int IDT, bool TIER>
+__global__ __launch_bounds__(kAlignThreads) void align_count_kernel(const void* __restrict__ ids, int64_t S,
+                                                                    int32_t n, const int32_t* __restrict__ lookup,
+                                                                    int32_t* __restrict__ ws) {
+  __shared__ int cnt[kAlignMaxExperts];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < n; e += kAlignThreads) cnt[e] = 0;
+  __syncthreads();
+  const int64_t i = (int64_t)blockIdx.x * kAlignThreads + tid;
+  if (i < S) {
+    const int64_t e = placed_id<IDT, TIER>(ids, i, n, lookup);
+    if (e >= 0) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  for (int e = tid; e < n; e += kAlignThreads) ws[(int64_t)blockIdx.x * n + e] = cnt[e];
+}
+
 // Places the slots of chunk blockIdx.x (1024 slots) after align_kernel<IDT, false> wrote the
 // block plan: the chunk's slots of each expert go after the expert's slots in earlier chunks
-// (counted again here), in slot order (per wave by ballot rank, then over the waves).
+// (read from the workspace's prefix when there is one, else counted again here), in slot order
+// (per wave by ballot rank, then over the waves).
 template <int IDT, bool TIER>
 __global__ __launch_bounds__(kAlignThreads) void align_scatter_kernel(const void* __restrict__ ids, int64_t S,
                                                                       int32_t n, const int32_t* __restrict__ lookup,
                                                                       int32_t bm, int64_t max_blocks,
                                                                       int32_t* __restrict__ sorted_ids,
                                                                       const int32_t* __restrict__ expert_ids,
-                                                                      const int32_t* __restrict__ npp) {
+                                                                      const int32_t* __restrict__ npp,
+                                                                      const int32_t* __restrict__ ws) {
   __shared__ int pre[kAlignMaxExperts];      // the expert's slots in earlier chunks
   __shared__ int start[kAlignMaxExperts];    // first padded row of the expert's run
   __shared__ int wcnt[kAlignWaves][kAlignMaxExperts];
@@ -299,16 +339,17 @@ __global__ __launch_bounds__(kAlignThreads) void align_scatter_kernel(const void
   while ((1 << nbits) <= n) ++nbits;
   const uint64_t below = (lane ? (~0ull >> (64 - lane)) : 0ull);
   const int64_t c0 = (int64_t)blockIdx.x * kAlignThreads;
-  for (int e = tid; e < n; e += kAlignThreads) pre[e] = 0;
+  for (int e = tid; e < n; e += kAlignThreads) pre[e] = ws ? ws[(int64_t)blockIdx.x * n + e] : 0;
   for (int e = lane; e < n; e += kWave) wcnt[w][e] = 0;
   __syncthreads();
   constexpr int kBatch = 16;
-  for (int64_t b0 = 0; b0 < c0; b0 += kBatch * kAlignThreads) {
+  const int64_t pre_end = ws ? 0 : c0;        // without a workspace: count the slots before the chunk
+  for (int64_t b0 = 0; b0 < pre_end; b0 += kBatch * kAlignThreads) {
     int64_t e[kBatch];
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
       const int64_t i = b0 + k * kAlignThreads + tid;
-      e[k] = i < c0 ? placed_id<IDT, TIER>(ids, i, n, lookup) : -1;
+      e[k] = i < pre_end ? placed_id<IDT, TIER>(ids, i, n, lookup) : -1;
     }
 #pragma unroll
     for (int k = 0; k < kBatch; ++k)
@@ -394,9 +435,16 @@ extern "C" int64_t bh_hex_align_max_blocks(int64_t S, int32_t n_experts, int32_t
   return cdiv(S, block_m) + (S < n_experts ? S : (int64_t)n_experts);
 }
 
+extern "C" int64_t bh_hex_align_workspace(int64_t S, int32_t n_experts) {
+  if (S < 0 || n_experts <= 0) return -1;
+  return S > kAlignSplit ? cdiv(S, kAlignThreads) * n_experts : 0;
+}
+
+// ws: null (the slots before each chunk are counted again by its placing workgroup), or
+// bh_hex_align_workspace(S, n) int32 values for the per-chunk counts.
 static int align_run(const char* who, const void* ids, int32_t ids_dtype, int64_t S, int32_t n_experts,
-                     const int32_t* lookup, int32_t block_m, int32_t* sorted_ids, int32_t* expert_ids, int32_t* npp,
-                     void* stream) {
+                     const int32_t* lookup, int32_t block_m, int32_t* ws, int64_t ws_len, int32_t* sorted_ids,
+                     int32_t* expert_ids, int32_t* npp, void* stream) {
   const std::string w(who);
   if (block_m <= 0) return fail(BH_HEX_ERR_VALUE, w + ": block_m must be positive");
   if (n_experts <= 0 || n_experts > kAlignMaxExperts)
@@ -409,20 +457,25 @@ static int align_run(const char* who, const void* ids, int32_t ids_dtype, int64_
   if (max_blocks * block_m > (int64_t)INT32_MAX) return fail(BH_HEX_ERR_VALUE, w + ": plan too large");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   // up to kAlignSplit slots one workgroup does everything; above, it writes the block plan and
-  // one workgroup per 1024 slots places them
+  // one workgroup per 1024 slots places them (with a workspace, one workgroup per 1024 slots
+  // first counts them, so that no workgroup counts more than its own chunk)
   const bool split = S > kAlignSplit;
+  if (!split) ws = nullptr;
+  if (ws && ws_len < bh_hex_align_workspace(S, n_experts)) return fail(BH_HEX_ERR_VALUE, w + ": workspace too small");
   const dim3 chunks((unsigned)cdiv(S, kAlignThreads));
   const dim3 one(1), threads(kAlignThreads);
 #define BH_ALIGN(IDT, TIER)                                                                                       \
   do {                                                                                                            \
     if (split) {                                                                                                  \
+      if (ws)                                                                                                     \
+        hipLaunchKernelGGL((align_count_kernel<IDT, TIER>), chunks, threads, 0, st, ids, S, n_experts, lookup, ws); \
       hipLaunchKernelGGL((align_kernel<IDT, false, TIER>), one, threads, 0, st, ids, S, n_experts, lookup,        \
-                         block_m, max_blocks, sorted_ids, expert_ids, npp);                                       \
+                         block_m, max_blocks, sorted_ids, expert_ids, npp, ws);                                   \
       hipLaunchKernelGGL((align_scatter_kernel<IDT, TIER>), chunks, threads, 0, st, ids, S, n_experts, lookup,    \
-                         block_m, max_blocks, sorted_ids, expert_ids, npp);                                       \
+                         block_m, max_blocks, sorted_ids, expert_ids, npp, ws);                                   \
     } else {                                                                                                      \
       hipLaunchKernelGGL((align_kernel<IDT, true, TIER>), one, threads, 0, st, ids, S, n_experts, lookup, block_m, \
-                         max_blocks, sorted_ids, expert_ids, npp);                                                \
+                         max_blocks, sorted_ids, expert_ids, npp, nullptr);                                       \
     }                                                                                                             \
   } while (0)
   if (lookup) {
@@ -438,15 +491,25 @@ static int align_run(const char* who, const void* ids, int32_t ids_dtype, int64_
 
 extern "C" int bh_hex_align(const void* ids, int32_t ids_dtype, int64_t S, int32_t n_experts, int32_t block_m,
                             int32_t* sorted_ids, int32_t* expert_ids, int32_t* npp, void* stream) {
-  return align_run("bh_hex_align", ids, ids_dtype, S, n_experts, nullptr, block_m, sorted_ids, expert_ids, npp, stream);
+  return align_run("bh_hex_align", ids, ids_dtype, S, n_experts, nullptr, block_m, nullptr, 0, sorted_ids, expert_ids,
+                   npp, stream);
 }
 
 extern "C" int bh_hex_align_tier(const void* ids, int32_t ids_dtype, int64_t S, int32_t n_experts,
                                  const int32_t* lookup, int32_t block_m, int32_t* sorted_ids, int32_t* expert_ids,
                                  int32_t* npp, void* stream) {
   if (!lookup) return fail(BH_HEX_ERR_VALUE, "bh_hex_align_tier: null lookup");
-  return align_run("bh_hex_align_tier", ids, ids_dtype, S, n_experts, lookup, block_m, sorted_ids, expert_ids, npp,
-                   stream);
+  return align_run("bh_hex_align_tier", ids, ids_dtype, S, n_experts, lookup, block_m, nullptr, 0, sorted_ids,
+                   expert_ids, npp, stream);
+}
+
+extern "C" int bh_hex_align_ws(const void* ids, int32_t ids_dtype, int64_t S, int32_t n_experts, const int32_t* lookup,
+                               int32_t block_m, int32_t* workspace, int64_t workspace_len, int32_t* sorted_ids,
+                               int32_t* expert_ids, int32_t* npp, void* stream) {
+  const int64_t need = bh_hex_align_workspace(S, n_experts);
+  if (need > 0 && !workspace) return fail(BH_HEX_ERR_VALUE, "bh_hex_align_ws: null workspace");
+  return align_run("bh_hex_align_ws", ids, ids_dtype, S, n_experts, lookup, block_m, workspace, workspace_len,
+                   sorted_ids, expert_ids, npp, stream);
 }
 
 extern "C" int bh_hex_direct(const void* ids, int32_t ids_dtype, int64_t S, int32_t block_m, int32_t* sorted_ids,

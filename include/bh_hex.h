@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define BH_HEX_ABI_VERSION 5
+#define BH_HEX_ABI_VERSION 6
 
 enum bh_hex_status {
   BH_HEX_OK = 0,
@@ -115,6 +115,20 @@ int bh_hex_align(const void* ids, int32_t ids_dtype, int64_t S, int32_t n_expert
  * which shares one plan between its tiers (hex_moe.py:318-324). */
 int bh_hex_align_tier(const void* ids, int32_t ids_dtype, int64_t S, int32_t n_experts, const int32_t* lookup,
                       int32_t block_m, int32_t* sorted_ids, int32_t* expert_ids, int32_t* npp, void* stream);
+
+/* int32 values of the workspace bh_hex_align_ws takes for S slots: ceil(S / 1024) * n_experts
+ * above 4096 slots, 0 up to 4096; -1 for bad sizes. */
+int64_t bh_hex_align_workspace(int64_t S, int32_t n_experts);
+
+/* bh_hex_align (lookup null) or bh_hex_align_tier (lookup given), same outputs, with a caller
+ * workspace of bh_hex_align_workspace(S, n_experts) int32 values (workspace_len of them; its
+ * contents on entry do not matter). Above 4096 slots one workgroup per 1024-slot chunk counts
+ * the chunk's slots per expert into it, so the placing workgroups read each chunk's prefix
+ * instead of counting every slot before their chunk. Replaces the same reference function
+ * (runtime/blackhole_runtime/hex_moe.py:201-222, align). */
+int bh_hex_align_ws(const void* ids, int32_t ids_dtype, int64_t S, int32_t n_experts, const int32_t* lookup,
+                    int32_t block_m, int32_t* workspace, int64_t workspace_len, int32_t* sorted_ids,
+                    int32_t* expert_ids, int32_t* npp, void* stream);
 
 /* One block per slot, no sorting (hex_moe.py:228-237, direct): sorted_ids[s * block_m] = s and S
  * elsewhere, expert_ids = ids as int32, npp = S * block_m. */

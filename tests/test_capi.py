@@ -44,6 +44,23 @@ def test_align_max_blocks_formula():
     assert lib.bh_hex_align_max_blocks(4, 4, 0) == -1
 
 
+def test_align_workspace_sizes_and_errors():
+    """bh_hex_align_ws: ceil(S / 1024) counts per expert above 4096 slots, none up to 4096; a
+    null or short workspace is refused before anything is launched."""
+    lib = _lib.load()
+    assert lib.bh_hex_align_workspace(4096, 96) == 0
+    assert lib.bh_hex_align_workspace(4097, 96) == 5 * 96
+    assert lib.bh_hex_align_workspace(32768, 96) == 32 * 96
+    assert lib.bh_hex_align_workspace(-1, 96) == -1 and lib.bh_hex_align_workspace(8, 0) == -1
+    fake = ctypes.c_void_p(16)          # never dereferenced: the checks return first
+    _status(lib.bh_hex_align_ws(fake, _lib.I64, 8192, 96, None, 128, None, 0, fake, fake, fake, None),
+            _lib.ERR_VALUE, "null workspace")
+    _status(lib.bh_hex_align_ws(fake, _lib.I64, 8192, 96, None, 128, fake, 8 * 96 - 1, fake, fake, fake, None),
+            _lib.ERR_VALUE, "workspace too small")
+    _status(lib.bh_hex_align_ws(fake, _lib.I64, 8192, 96, None, 0, fake, 8 * 96, fake, fake, fake, None),
+            _lib.ERR_VALUE, "block_m")
+
+
 def _workspace(lib, *args):
     nc, npart = ctypes.c_int64(), ctypes.c_int64()
     rc = lib.bh_hex_moe_workspace(*args, ctypes.byref(nc), ctypes.byref(npart))

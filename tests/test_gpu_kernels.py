@@ -119,9 +119,11 @@ def test_align_bit_exact(S, n, bm, skew, idt):
         p /= p.sum()
     ids = rng.choice(n, S, p=p) if S else np.zeros(0, np.int64)
     want = O.align(ids, n, bm)
-    got = hm.align(torch.from_numpy(ids).to(idt).to(DEV), n, bm)
-    for g, w in zip(got, want):
-        assert np.array_equal(g.cpu().numpy(), w)
+    # above 4096 slots: counted per chunk into a workspace, and without one
+    for chunked in ((True, False) if S > 4096 else (True,)):
+        got = hm.align(torch.from_numpy(ids).to(idt).to(DEV), n, bm, _chunked=chunked)
+        for g, w in zip(got, want):
+            assert np.array_equal(g.cpu().numpy(), w), chunked
 
 
 @pytest.mark.parametrize("S,n,bm", [(128, 96, 16), (2048, 96, 32), (9000, 96, 128), (40000, 128, 64), (50, 8, 16)])
@@ -143,10 +145,11 @@ def test_align_tier_bit_exact(S, n, bm):
     want_sid[: s_sub.size] = np.where(s_sub < sub.size, sub[np.minimum(s_sub, max(sub.size - 1, 0))], S)
     want_eid = np.full(mb, -1, np.int32)
     want_eid[: e_sub.size] = e_sub
-    sid, eid, npp = hm.align(torch.from_numpy(ids).to(DEV), n, bm, torch.from_numpy(lookup).to(DEV))
-    assert np.array_equal(sid.cpu().numpy(), want_sid)
-    assert np.array_equal(eid.cpu().numpy(), want_eid)
-    assert npp.item() == int(npp_sub[0])
+    for chunked in ((True, False) if S > 4096 else (True,)):
+        sid, eid, npp = hm.align(torch.from_numpy(ids).to(DEV), n, bm, torch.from_numpy(lookup).to(DEV), chunked)
+        assert np.array_equal(sid.cpu().numpy(), want_sid), chunked
+        assert np.array_equal(eid.cpu().numpy(), want_eid), chunked
+        assert npp.item() == int(npp_sub[0]), chunked
 
 
 def test_align_reference_example():
