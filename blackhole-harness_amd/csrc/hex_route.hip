@@ -224,22 +224,42 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(const void* __rest
     }
   } else if (ws) {
     // align_count_kernel's counts per 1024-slot chunk -> each chunk's exclusive prefix per
-    // expert (in place, read by align_scatter_kernel) and the totals
+    // expert (in place, read by align_scatter_kernel) and the totals. When they fit, the counts
+    // pass through the (here unused) per-wave counter array in LDS: one round trip to the
+    // workspace each way, with every thread loading, instead of one per 8 chunks per expert.
     const int nch = (int)((S + kAlignThreads - 1) / kAlignThreads);
-    for (int e = tid; e < n; e += kAlignThreads) {
-      int acc = 0;
-      for (int c0 = 0; c0 < nch; c0 += 8) {
-        int v[8];
-#pragma unroll
-        for (int d = 0; d < 8; ++d) v[d] = c0 + d < nch ? ws[(int64_t)(c0 + d) * n + e] : 0;
-#pragma unroll
-        for (int d = 0; d < 8; ++d)
-          if (c0 + d < nch) {
-            ws[(int64_t)(c0 + d) * n + e] = acc;
-            acc += v[d];
-          }
+    const int nv = nch * n;
+    int* const lc = &wcnt[0][0];
+    if (nv <= kAlignWaves * kAlignMaxExperts) {
+      for (int v = tid; v < nv; v += kAlignThreads) lc[v] = ws[v];
+      __syncthreads();
+      for (int e = tid; e < n; e += kAlignThreads) {
+        int acc = 0;
+        for (int c = 0; c < nch; ++c) {
+          const int v = lc[c * n + e];
+          lc[c * n + e] = acc;
+          acc += v;
+        }
+        cnt[e] = acc;
       }
-      cnt[e] = acc;
+      __syncthreads();
+      for (int v = tid; v < nv; v += kAlignThreads) ws[v] = lc[v];
+    } else {
+      for (int e = tid; e < n; e += kAlignThreads) {
+        int acc = 0;
+        for (int c0 = 0; c0 < nch; c0 += 8) {
+          int v[8];
+#pragma unroll
+          for (int d = 0; d < 8; ++d) v[d] = c0 + d < nch ? ws[(int64_t)(c0 + d) * n + e] : 0;
+#pragma unroll
+          for (int d = 0; d < 8; ++d)
+            if (c0 + d < nch) {
+              ws[(int64_t)(c0 + d) * n + e] = acc;
+              acc += v[d];
+            }
+        }
+        cnt[e] = acc;
+      }
     }
   } else {
     for (int e = tid; e < n; e += kAlignThreads) cnt[e] = 0;
