@@ -388,6 +388,7 @@ def hex_moe_fused(x, topk_weights, topk_ids, tiers: list[HexTier], config: dict 
     if (LAYER and len(tiers) == 1 and bm1 == bm2 == 16 and S <= LAYER_MAX_SLOTS and align_mode == "auto"
             and _launch_layer(x, w, flat, tiers[0], act, y, out, T, k)):
         return out
+
     def run_tier(t: HexTier, lk: torch.Tensor | None) -> None:
         # one plan per tier when there are several, so each tier's launches walk only its blocks
         p1 = plan(flat, E, bm1, align_mode, lk)
