@@ -38,6 +38,7 @@ HEX_BLOCK = 32     # inputs per bit stream (blackhole/anatomy/hex.py:44)
 DIRECT_MAX = int(os.environ.get("BLACKHOLE_HEX_DIRECT_MAX", "32"))      # slots (hex_moe.py:260)
 DEQUANT_MIN = int(os.environ.get("BLACKHOLE_HEX_DEQUANT_MIN", "1024"))  # slots (hex_moe.py:261)
 PREFILL_MIN = 64     # slots per expert above which the fused path takes the 128-slot prefill kernels
+DECODE16_MAX = 12    # slots per expert up to which the decode kernels take 16-slot blocks
 # one launch per layer (plan, gate/up, down, sum) for one tier at 16-slot blocks and few slots;
 # opt-in: on MI355X it measured 91 us per config-2 T=16 layer against 72 us for the four launches
 LAYER = os.environ.get("BLACKHOLE_HEX_LAYER", "0") != "0"
@@ -222,13 +223,16 @@ def default_config(slots: int, n_out: int, n_in: int, glu: bool, n_experts: int 
     """Tile choice by slot count (hex_moe.py:264-283), or BLACKHOLE_HEX_TILES="BM". BLOCK_M grows
     with the slots each expert gets, so an expert's weights are streamed by few blocks. 64-slot
     blocks are never chosen by default: on MI355X their gate/up kernel spills registers and ran
-    over twice as long as 32-slot blocks on config 4's batch."""
+    over twice as long as 32-slot blocks on config 4's batch. 16-slot blocks up to 12 slots per
+    expert on average: at 16 (config 5, T=256) the experts that get more than 16 slots stream
+    their weights twice, and 32-slot blocks measured 352 against 434 us; at 10.7 (config 2,
+    T=128) the two tie, and at 5.3 (T=64) 16-slot blocks win, 91 against 97 us."""
     env = os.environ.get("BLACKHOLE_HEX_TILES")
     if env:
         bm = _tile_from({"BLOCK_M": int(env.split(",")[0])})
     else:
         per_expert = slots / max(1, n_experts or slots)
-        bm = 16 if per_expert <= 16 else (32 if per_expert <= PREFILL_MIN else 128)
+        bm = 16 if per_expert <= DECODE16_MAX else (32 if per_expert <= PREFILL_MIN else 128)
     return {"BLOCK_M": _fit_tile(bm, n_in, n_out, glu), "BLOCK_N": 256}
 
 

@@ -54,6 +54,8 @@ def test_block_from_shapes_128():
 def test_default_config_and_env(monkeypatch):
     assert hm.default_config(8, 768, 2048, True, 96) == {"BLOCK_M": 16, "BLOCK_N": 256}    # T=1 decode
     assert hm.default_config(128, 768, 2048, True, 96)["BLOCK_M"] == 16                    # T=16
+    assert hm.default_config(96 * 12, 768, 2048, True, 96)["BLOCK_M"] == 16                # 12 per expert
+    assert hm.default_config(2048, 1536, 4096, True, 128)["BLOCK_M"] == 32                 # 16 per expert
     assert hm.default_config(32768, 2048, 768, False, 96)["BLOCK_M"] == 128                # prefill
     assert hm.default_config(32768, 2048, 96, False, 96)["BLOCK_M"] == 32                  # inputs % 128 != 0
     assert hm.default_config(3000, 768, 2048, True, 96)["BLOCK_M"] == 32
