@@ -37,7 +37,7 @@ HEX_BLOCK = 32     # inputs per bit stream (blackhole/anatomy/hex.py:44)
 
 DIRECT_MAX = int(os.environ.get("BLACKHOLE_HEX_DIRECT_MAX", "32"))      # slots (hex_moe.py:260)
 DEQUANT_MIN = int(os.environ.get("BLACKHOLE_HEX_DEQUANT_MIN", "1024"))  # slots (hex_moe.py:261)
-PREFILL_MIN = 64     # slots per expert above which the fused path takes the 128-slot prefill kernels
+PREFILL_MIN = 40     # slots per expert above which the fused path takes the 128-slot prefill kernels
 DECODE16_MAX = 12    # slots per expert up to which the decode kernels take 16-slot blocks
 # one launch per layer (plan, gate/up, down, sum) for one tier at 16-slot blocks and few slots;
 # opt-in: on MI355X it measured 91 us per config-2 T=16 layer against 72 us for the four launches
@@ -226,7 +226,9 @@ def default_config(slots: int, n_out: int, n_in: int, glu: bool, n_experts: int 
     over twice as long as 32-slot blocks on config 4's batch. 16-slot blocks up to 12 slots per
     expert on average: at 16 (config 5, T=256) the experts that get more than 16 slots stream
     their weights twice, and 32-slot blocks measured 352 against 434 us; at 10.7 (config 2,
-    T=128) the two tie, and at 5.3 (T=64) 16-slot blocks win, 91 against 97 us."""
+    T=128) the two tie, and at 5.3 (T=64) 16-slot blocks win, 91 against 97 us. The 128-slot
+    prefill kernels above 40 slots per expert: at 64 (config 5, T=1024) 728 against 890 us on
+    32-slot blocks, at 42.7 (config 2, T=512) a tie, at 32 (config 5, T=512) 690 against 550."""
     env = os.environ.get("BLACKHOLE_HEX_TILES")
     if env:
         bm = _tile_from({"BLOCK_M": int(env.split(",")[0])})

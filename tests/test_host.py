@@ -58,8 +58,9 @@ def test_default_config_and_env(monkeypatch):
     assert hm.default_config(2048, 1536, 4096, True, 128)["BLOCK_M"] == 32                 # 16 per expert
     assert hm.default_config(32768, 2048, 768, False, 96)["BLOCK_M"] == 128                # prefill
     assert hm.default_config(32768, 2048, 96, False, 96)["BLOCK_M"] == 32                  # inputs % 128 != 0
-    assert hm.default_config(3000, 768, 2048, True, 96)["BLOCK_M"] == 32
-    assert hm.default_config(6000, 768, 2048, True, 96)["BLOCK_M"] == 32                   # (64 never by default)
+    assert hm.default_config(3000, 768, 2048, True, 96)["BLOCK_M"] == 32                   # 31 per expert
+    assert hm.default_config(96 * 40, 768, 2048, True, 96)["BLOCK_M"] == 32                # 40 per expert
+    assert hm.default_config(96 * 41, 768, 2048, True, 96)["BLOCK_M"] == 128               # (64 never by default)
     monkeypatch.setenv("BLACKHOLE_HEX_TILES", "64")
     assert hm.default_config(8, 768, 2048, True, 96) == {"BLOCK_M": 64, "BLOCK_N": 256}
     # the reference's own config keys map onto the tile
