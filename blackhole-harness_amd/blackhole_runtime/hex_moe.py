@@ -16,7 +16,11 @@ fused   the HIP kernels: slot plan (direct for a handful of slots, else the alig
 dequant every expert decoded once by the dequant kernel into bf16/f16/f32 stacks, then one
         matrix product per routed expert (rocBLAS through torch). It is taken for float32
         activations (the fused kernels run the matrix cores in bf16/f16), for path="dequant", and
-        by path="auto" at or above BLACKHOLE_HEX_DEQUANT_MIN slots outside graph capture.
+        by path="auto" at or above BLACKHOLE_HEX_DEQUANT_MIN slots outside graph capture when
+        that variable is set. Unset, path="auto" keeps to the fused kernels at every batch: the
+        reference switches at 1024 slots because its fused Triton kernel slows down at large
+        batches, while here the prefill kernels take over there, and the dequant path measured
+        15 ms per layer against 0.1-0.5 ms fused (config 2 at 128 and 1024 tokens, config 3).
 
 Everything runs on the GPU; CPU tensors are refused (the reference's CPU route is its
 Triton interpreter, whose role the tests give to the numpy oracle).
@@ -36,7 +40,8 @@ PROJS = ("gate_proj", "up_proj", "down_proj")
 HEX_BLOCK = 32     # inputs per bit stream (blackhole/anatomy/hex.py:44)
 
 DIRECT_MAX = int(os.environ.get("BLACKHOLE_HEX_DIRECT_MAX", "32"))      # slots (hex_moe.py:260)
-DEQUANT_MIN = int(os.environ.get("BLACKHOLE_HEX_DEQUANT_MIN", "1024"))  # slots (hex_moe.py:261)
+# slots from which path="auto" takes the dequant path (hex_moe.py:261); never unless set
+DEQUANT_MIN = int(os.environ.get("BLACKHOLE_HEX_DEQUANT_MIN", str(1 << 62)))
 PREFILL_MIN = 40     # slots per expert above which the fused path takes the 128-slot prefill kernels
 DECODE16_MAX = 12    # slots per expert up to which the decode kernels take 16-slot blocks
 # one launch per layer (plan, gate/up, down, sum) for one tier at 16-slot blocks and few slots;
@@ -502,7 +507,8 @@ def hex_moe_dequant(x, topk_weights, topk_ids, tiers: list[HexTier]) -> torch.Te
 def hex_moe(x: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor, tiers: list[HexTier],
             config: dict | None = None, path: str = "auto") -> torch.Tensor:
     """Routed-expert output [T, H] of a SwiGLU MoE layer whose experts are HEX tiers (prepared)
-    (hex_moe.py:374-382). path: "auto" (fused below DEQUANT_MIN slots, else dequant, never
+    (hex_moe.py:374-382). path: "auto" (fused below DEQUANT_MIN slots, which is unbounded unless
+    BLACKHOLE_HEX_DEQUANT_MIN is set, else dequant, never
     dequant while capturing a graph; float32 activations always dequant), "fused" or "dequant"."""
     if path not in ("auto", "fused", "dequant"):
         raise ValueError(f"unknown path {path!r}")
