@@ -47,9 +47,10 @@ DECODE16_MAX = 12    # slots per expert up to which the decode kernels take 16-s
 # one launch per layer (plan, gate/up, down, sum) for one tier at 16-slot blocks and few slots;
 # opt-in: on MI355X it measured 91 us per config-2 T=16 layer against 72 us for the four launches
 LAYER = os.environ.get("BLACKHOLE_HEX_LAYER", "0") != "0"
-# a single tier's experts run as two halves on two streams through the prefill kernels (see
-# hex_moe_fused)
-SPLIT = os.environ.get("BLACKHOLE_HEX_SPLIT", "1") != "0"
+# a single tier's experts run as SPLIT parts on as many streams through the prefill kernels (see
+# hex_moe_fused); 1 or less keeps the tier whole. Two parts measured best: 433 / 439 / 447 us for
+# 2 / 3 / 4 parts at config 3, 1116 / 1136 / 1155 us at config 5 (T=2048).
+SPLIT = int(os.environ.get("BLACKHOLE_HEX_SPLIT", "2"))
 LAYER_MAX_SLOTS = 512
 
 
@@ -80,9 +81,9 @@ class HexTier:
     lookup: torch.Tensor | None = None
     _structs: dict = field(default_factory=dict, repr=False, compare=False)
     _experts_host: torch.Tensor | None = field(default=None, repr=False, compare=False)
-    # the tier's two halves by expert (views of the same tensors), for hex_moe_fused's streams
-    _halves: list | None = field(default=None, repr=False, compare=False)
-    _is_half: bool = field(default=False, repr=False, compare=False)
+    # the tier's SPLIT parts by expert (views of the same tensors), for hex_moe_fused's streams
+    _parts: list | None = field(default=None, repr=False, compare=False)
+    _is_part: bool = field(default=False, repr=False, compare=False)
 
     def prepare(self, num_experts: int) -> "HexTier":
         """Kernel-ready views (uint32 words as int32, float32 scales and levels, contiguous) and
@@ -112,15 +113,15 @@ class HexTier:
         self.experts = self.experts.to(dev).to(torch.int32)
         self._structs = {name: _proj_struct(getattr(self, name), self.bits) for name in PROJS}
         n = len(self.experts)
-        if not self._is_half and n >= 2:
-            self._halves = [self._part(0, n // 2, num_experts), self._part(n // 2, n, num_experts)]
+        if not self._is_part and SPLIT > 1 and n >= SPLIT:
+            self._parts = [self._part(n * j // SPLIT, n * (j + 1) // SPLIT, num_experts) for j in range(SPLIT)]
         return self
 
     def _part(self, lo: int, hi: int, num_experts: int) -> "HexTier":
         """Experts lo..hi-1 of the tier as a tier of their own (views, no copies)."""
         sub = HexTier(self.bits, self.experts[lo:hi],
                       *[{q: v[lo:hi] for q, v in getattr(self, name).items()} for name in PROJS])
-        sub._is_half = True
+        sub._is_part = True
         return sub.prepare(num_experts)
 
     def struct(self, name: str) -> _lib.HexProj:
@@ -274,12 +275,12 @@ _LAYER_WORKSPACES: dict = {}
 _SIDE_STREAMS: dict = {}
 
 
-def _side_stream(device: torch.device) -> torch.cuda.Stream:
-    """The second stream of a device (default priority) that runs the launches of a layer's
-    second and later tiers."""
-    s = _SIDE_STREAMS.get(device.index)
+def _side_stream(device: torch.device, i: int = 1) -> torch.cuda.Stream:
+    """Side stream i of a device (default priority): it runs the launches of a layer's tier (or
+    part of a tier) i."""
+    s = _SIDE_STREAMS.get((device.index, i))
     if s is None:
-        s = _SIDE_STREAMS[device.index] = torch.cuda.Stream(device)
+        s = _SIDE_STREAMS[(device.index, i)] = torch.cuda.Stream(device)
     return s
 
 
@@ -407,27 +408,28 @@ def hex_moe_fused(x, topk_weights, topk_ids, tiers: list[HexTier], config: dict 
         _launch_glu(x, act, t, *p1, S, k, bm1)
         _launch_down(act, y, t, *p2, S, w, bm2)
 
-    # Each slot is served by one tier, so the tiers write disjoint rows of act and y: the later
-    # tiers run on a side stream beside the first (each stream keeps its own workspace), which
-    # overlaps one tier's ramp and tail with the other's streaming (config 4's two tiers:
-    # 170 -> 144 us). Through the prefill kernels a single tier runs the same way as its two
-    # halves by expert, so that one half's grid tail overlaps the other's tiles (config 3:
-    # 476 -> 465 us); the persistent decode kernels each fill the GPU, and halves of them run
-    # one after the other (config 2, T=16: 71 -> 105 us), so a decode tier stays whole. The
-    # caller's stream waits for the side stream before the k-slot sum.
-    halves = SPLIT and bm1 == 128 and bm2 == 128 and tiers[0]._halves
-    chains = tiers if len(tiers) > 1 else (tiers[0]._halves if halves else tiers)
+    # Each slot is served by one tier, so the tiers write disjoint rows of act and y: each later
+    # tier runs on a side stream of its own beside the first (each stream keeps its own
+    # workspace), which overlaps one tier's ramp and tail with the other's streaming (config 4's
+    # two tiers: 170 -> 144 us). Through the prefill kernels a single tier runs the same way as
+    # its SPLIT parts by expert, so that one part's grid tail overlaps another's tiles (config 3,
+    # two parts: 476 -> 465 us); the persistent decode kernels each fill the GPU, and parts of
+    # them run one after the other (config 2, T=16: 71 -> 105 us), so a decode tier stays whole.
+    # The caller's stream waits for the side streams before the k-slot sum.
+    split = SPLIT > 1 and bm1 == 128 and bm2 == 128 and tiers[0]._parts
+    chains = tiers if len(tiers) > 1 else (tiers[0]._parts if split else tiers)
     if len(chains) == 1:
         run_tier(chains[0], None)
     else:
         main = torch.cuda.current_stream(x.device)
-        side = _side_stream(x.device)
-        side.wait_stream(main)
-        with torch.cuda.stream(side):
-            for t in chains[1:]:
+        sides = [_side_stream(x.device, i) for i in range(1, len(chains))]
+        for side, t in zip(sides, chains[1:]):
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
                 run_tier(t, t.lookup)
         run_tier(chains[0], chains[0].lookup)
-        main.wait_stream(side)
+        for side in sides:
+            main.wait_stream(side)
     ids, code = _ids_arg(flat)
     lib = _lib.load()
     _lib.check(lib.bh_hex_moe_reduce(y.data_ptr(), _lib.dtype_code(y.dtype), y.stride(0), ids.data_ptr(), code, E, T, k,

@@ -398,7 +398,7 @@ def test_graph_capture_replays_match_eager(bm, split):
     cfg = None if bm is None else {"BLOCK_M": bm}
     ref, tiers = make_layer(E, H, I, split, (4, 3), seed=12)
     if bm == 128 and split == 0:
-        assert len(tiers) == 1 and tiers[0]._halves and hm.SPLIT
+        assert len(tiers) == 1 and tiers[0]._parts and hm.SPLIT > 1
         assert run_fused(ref, tiers, T, E, k, H, seed=5, config=cfg) < TOL_16
     w, ids = routing(T, E, k, seed=5)
     x = torch.randn(T, H, generator=torch.Generator().manual_seed(0)).to(torch.bfloat16).to(DEV)
