@@ -420,6 +420,36 @@ def test_graph_capture_replays_match_eager(bm, split):
         torch.cuda.synchronize()
 
 
+def test_three_tiers_on_three_streams():
+    """Three tiers (4, 3 and 4 bits): the second and third run on side streams of their own,
+    eager and captured in a hipGraph, decode and prefill tiles."""
+    say("three tiers")
+    E, H, I, k = 12, 256, 128, 3
+    perm = np.random.default_rng(51).permutation(E)
+    ref, tiers = [], []
+    for j, (ids, b) in enumerate(zip(np.split(perm, 3), (4, 3, 4))):
+        parts = {proj: O.random_parts(len(ids), o, i, b, seed=510 + 10 * j + q, block=128)
+                 for q, (proj, (o, i)) in enumerate((("gate_proj", (I, H)), ("up_proj", (I, H)), ("down_proj", (H, I))))}
+        ref.append({"bits": b, "experts": ids, **parts})
+        tiers.append(hm.HexTier(b, torch.from_numpy(ids.astype(np.int32)),
+                                *[dev_parts(parts[p]) for p in ("gate_proj", "up_proj", "down_proj")]).prepare(E))
+    for T, cfg in ((20, None), (500, {"BLOCK_M": 128})):
+        assert run_fused(ref, tiers, T, E, k, H, seed=T, config=cfg) < TOL_16, T
+        w, ids = routing(T, E, k, seed=T)
+        x = torch.randn(T, H, generator=torch.Generator().manual_seed(T)).to(torch.bfloat16).to(DEV)
+        wd, idd = torch.from_numpy(w).to(DEV), torch.from_numpy(ids).to(DEV)
+        eager = hm.hex_moe_fused(x, wd, idd, tiers, cfg)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            out = hm.hex_moe_fused(x, wd, idd, tiers, cfg)
+        for i in range(2):
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager), (T, i)
+            _ = hm.hex_moe_fused(x * 2, wd, idd, tiers, cfg)
+            torch.cuda.synchronize()
+
+
 # --------------------------------------------------------------------------- one-launch layer
 
 
