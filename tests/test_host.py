@@ -42,6 +42,23 @@ def test_prepare_views_lookup_and_structs():
         _tier([0], 3).__class__(4, torch.tensor([0]), *[_parts(1, 8, 64, 3, 1)] * 3).prepare(2)
 
 
+def test_prepare_splits_experts_into_parts():
+    """prepare() also builds the tier's SPLIT parts by expert for the prefill streams: views of
+    the tier's own tensors (no copies), each with the lookup of its own experts."""
+    t = _tier([3, 0, 5, 1, 4], 4).prepare(6)
+    assert hm.SPLIT == 2 and len(t._parts) == 2
+    a, b = t._parts
+    assert a.experts.tolist() == [3, 0] and b.experts.tolist() == [5, 1, 4]
+    assert a.lookup.tolist() == [1, -1, -1, 0, -1, -1] and b.lookup.tolist() == [-1, 1, -1, -1, 2, 0]
+    for name in hm.PROJS:
+        whole, pa, pb = getattr(t, name), getattr(a, name), getattr(b, name)
+        for q in ("idx", "block_scale", "expert_scale", "levels"):
+            assert pa[q].data_ptr() == whole[q].data_ptr()
+            assert pb[q].data_ptr() == whole[q][2:].data_ptr() and torch.equal(pb[q], whole[q][2:])
+    assert a._parts is None and b._parts is None             # parts are not split again
+    assert _tier([2], 4).prepare(6)._parts is None           # one expert: nothing to split
+
+
 def test_block_from_shapes_128():
     t = _tier([0], 4, H=256, I=128)
     for name in ("gate_proj", "up_proj", "down_proj"):
