@@ -414,7 +414,8 @@ def hex_moe_fused(x, topk_weights, topk_ids, tiers: list[HexTier], config: dict 
     # two tiers: 170 -> 144 us). Through the prefill kernels a single tier runs the same way as
     # its SPLIT parts by expert, so that one part's grid tail overlaps another's tiles (config 3,
     # two parts: 476 -> 465 us); the persistent decode kernels each fill the GPU, and parts of
-    # them run one after the other (config 2, T=16: 71 -> 105 us), so a decode tier stays whole.
+    # them run one after the other (config 2, T=16: 71 -> 105 us; on 32-slot blocks config 2,
+    # T=256: 119 -> 136 us), so a decode tier stays whole.
     # The caller's stream waits for the side streams before the k-slot sum.
     split = SPLIT > 1 and bm1 == 128 and bm2 == 128 and tiers[0]._parts
     chains = tiers if len(tiers) > 1 else (tiers[0]._parts if split else tiers)
