@@ -42,6 +42,10 @@ CONFIGS = {
 }
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+# Untimed warm-up before every timed point: at least --warmup layer calls, and replays for at
+# least this long, so the GPU's clocks have settled whatever the batch size (a point timed after
+# three replays of a long prefill layer measured 16% slower than after forty).
+WARMUP_FLOOR_S = 0.3
 
 
 def log(msg: str) -> None:
@@ -140,11 +144,24 @@ def graph_of(fn):
     return g
 
 
+def warm(g, calls_per_replay: int, min_calls: int) -> int:
+    """Replays graph g (untimed) until it has run at least min_calls layer calls and
+    WARMUP_FLOOR_S seconds; returns the calls run."""
+    import torch
+    calls, t0 = 0, time.perf_counter()
+    while calls < min_calls or time.perf_counter() - t0 < WARMUP_FLOOR_S:
+        g.replay()
+        calls += calls_per_replay
+        if calls >= min_calls:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return calls
+
+
 def event_time_ms(g, reps: int) -> float:
     """Average milliseconds per replay of graph g, from HIP events on the current stream."""
     import torch
-    g.replay()
-    torch.cuda.synchronize()
+    warm(g, 1, 1)
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
     for _ in range(reps):
@@ -217,9 +234,7 @@ def run_layer(cfg, copies, T, steps, warmup, block, breakdown=True):
     g = graph_of(layers(n))
     rem = steps % n                          # exactly `steps` layer calls: full replays + one partial
     g_rem = graph_of(layers(rem)) if rem else None
-    for _ in range(max(1, -(-warmup // n))):
-        g.replay()
-    torch.cuda.synchronize()
+    warm_calls = warm(g, n, warmup)
     t0 = time.perf_counter()
     for _ in range(steps // n):
         g.replay()
@@ -232,13 +247,32 @@ def run_layer(cfg, copies, T, steps, warmup, block, breakdown=True):
     total, glu_b, used = layer_bytes(cfg, copies[0], ids, block, T)
     S = T * cfg["k"]
     flops = 6.0 * S * cfg["H"] * cfg["I"]
-    out = {"T": T, "steps": calls, "ms_per_step": ms, "tokens_per_s": T / (ms * 1e-3), "unique_experts": used,
+    out = {"T": T, "steps": calls, "warmup_calls": warm_calls, "ms_per_step": ms, "tokens_per_s": T / (ms * 1e-3),
+           "unique_experts": used,
            "layer_bytes": total, "hbm_gbps": total / (ms * 1e-3) / 1e9,
            "hbm_frac": total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
            "mfma_frac": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, "glu_bytes": glu_b}
     if breakdown:
         out["kernels"] = kernel_breakdown(cfg, copies, x, w, ids, max(5, steps // (2 * n)))
     return out, (x, w, ids, logits)
+
+
+def prefill_roofline(cfg, T, kernels):
+    """Roofline entry of the dominant prefill kernel (the gate/up kernel over the whole tier):
+    useful matrix flops per launch (4 S H I: gate and up) over its average launch time from HIP
+    events, against the bf16 peak; with the counter-measured matrix-core busy fraction of the same
+    kernel when its summary is in profiles/."""
+    S = T * cfg["k"]
+    flops = 4.0 * S * cfg["H"] * cfg["I"]
+    us = kernels["glu_us"]
+    tf = flops / (us * 1e-6) / 1e12
+    busy = json.loads(MFMA_FILE.read_text()) if MFMA_FILE.exists() else None
+    return {"bound": "mfma", "achieved": tf, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": tf / BF16_PEAK_TFLOPS, "kernel": f"{PREFILL_GLU_KERNEL} (gate/up + SiLU, 128-slot blocks)",
+            "workload": f"config3 T={T}", "flops_per_launch": flops, "avg_launch_us": us,
+            "down_us": kernels["down_us"], "plan_us": kernels["plan_us"],
+            "mfma_busy_frac": busy["mfma_busy_frac"] if busy else None,
+            "mfma_busy_source": str(MFMA_FILE.relative_to(ROOT)) if busy else None}
 
 
 def cpu_threads() -> int:
@@ -294,7 +328,11 @@ def cpu_baseline(cfg, tiers, x, w, ids, budget_s=12.0):
 
 PROFILES = ROOT / "profiles"
 TRAFFIC_FILE = PROFILES / "hex_moe_glu_config2_T16_traffic.json"
+MFMA_FILE = PROFILES / "hex_gemm_glu_config3_T4096_mfma.json"
 GLU_KERNEL = "hex_moe_kernel<4, 1, true, 1, 4, true>"      # gate/up, 4-bit, bf16, block_m 16, 128-input scales
+PREFILL_GLU_KERNEL = "hex_gemm_kernel<3, 1, true, 4>"       # gate/up, 3-bit, bf16, 128-input scales
+SIMDS = 1024                                                 # MI355X: 256 CUs x 4 SIMDs
+XCDS = 8
 COPY_BYTES = 2 * (128 << 20) * 2                             # the calibration kernel: 256 MiB read + 256 MiB written
 
 
@@ -338,6 +376,21 @@ def rocprof_summary(dirs: list[str]) -> str:
                 if any(s in k for s in ("hex_moe", "hex_gemm", "align_", "moe_reduce", "bitwise_not")):
                     out.append(f"{k:<112} {c:<12} {sum(v) / len(v):>14.1f}  (n={len(v)})")
                 counters.setdefault(c, {})[k] = v
+    if "SQ_VALU_MFMA_BUSY_CYCLES" in counters and "GRBM_GUI_ACTIVE" in counters:
+        # matrix-core busy fraction of the prefill gate/up kernel: busy cycles (summed over the
+        # SIMDs) over SIMDs x the kernel's GPU-busy cycles (GRBM_GUI_ACTIVE sums the XCDs)
+        busy = {k: v for k, v in counters["SQ_VALU_MFMA_BUSY_CYCLES"].items() if PREFILL_GLU_KERNEL in k}
+        grbm = {k: v for k, v in counters["GRBM_GUI_ACTIVE"].items() if PREFILL_GLU_KERNEL in k}
+        if busy and grbm:
+            k = next(iter(busy))
+            b = sum(busy[k]) / len(busy[k])
+            gg = sum(grbm[k]) / len(grbm[k])
+            res = {"kernel": k, "mfma_busy_cycles": b, "grbm_gui_active": gg, "simds": SIMDS, "xcds": XCDS,
+                   "mfma_busy_frac": b / (SIMDS * gg / XCDS), "dispatches": len(busy[k])}
+            out.append("## matrix-core busy fraction of the prefill gate/up kernel")
+            out.append(json.dumps(res, indent=1))
+            PROFILES.mkdir(exist_ok=True)
+            MFMA_FILE.write_text(json.dumps(res) + "\n")
     if "FETCH_SIZE" in counters and "WRITE_SIZE" in counters:
         def kernel(c, pred):
             cand = {k: v for k, v in counters[c].items() if pred(k)}
@@ -415,6 +468,7 @@ def main(argv=None) -> int:
                 "avg_launch_us": k["glu_us"]}
 
     sweep = {}
+    roofline_prefill = None
     if not a.no_sweep and a.config == 2:
         for Ts in (1, 4, 64):
             r, _ = run_layer(cfg, copies, Ts, max(80, a.steps // 4), a.warmup, a.block, breakdown=False)
@@ -428,8 +482,10 @@ def main(argv=None) -> int:
         for c, n_copies, batches, steps in ((3, 2, (4096,), 16), (4, 4, (256,), 100), (5, 8, (1, 16, 256, 2048, 8192), 32)):
             layers = build_tiers(CONFIGS[c], a.block, n_copies, dev)
             for Ts in batches:
-                r, _ = run_layer(CONFIGS[c], layers, Ts, steps, a.warmup, a.block, breakdown=False)
+                r, _ = run_layer(CONFIGS[c], layers, Ts, steps, a.warmup, a.block, breakdown=c == 3)
                 sweep[f"config{c}_T{Ts}"] = {kk: r[kk] for kk in keys}
+                if c == 3:
+                    roofline_prefill = prefill_roofline(CONFIGS[c], Ts, r["kernels"])
                 log(f"  config{c} T={Ts}: {r['ms_per_step'] * 1e3:.1f} us/layer, {r['hbm_gbps']:.0f} GB/s "
                     f"({r['hbm_frac'] * 100:.1f}% of HBM), MFMA {r['mfma_frac'] * 100:.1f}% of bf16 peak")
             del layers
@@ -453,7 +509,8 @@ def main(argv=None) -> int:
     line = {
         "metric": "HEX MoE layer tokens/s; HBM GB/s @ decode b=16; MFMA util @ 4k prefill",
         "value": head["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": head["steps"],
-        "warmup": a.warmup, "ms_per_step": head["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+        "warmup": a.warmup, "warmup_floor_s": WARMUP_FLOOR_S, "warmup_calls": head["warmup_calls"],
+        "ms_per_step": head["ms_per_step"], "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic: seeded N(0,0.02) weights HEX-quantized on the GPU, bf16 N(0,1) activations, "
                 "N(0,1) router logits through the softmax top-k kernel",
@@ -463,7 +520,7 @@ def main(argv=None) -> int:
                    "tokens": T, "unique_experts": head["unique_experts"], "path": "fused"},
         "hbm_gbps_layer": head["hbm_gbps"], "hbm_frac_layer": head["hbm_frac"],
         "kernels_us": {kk: v for kk, v in k.items() if kk.endswith("_us")}, "tiles": k["tiles"],
-        "roofline": roofline, "cpu_baseline": cpu, "sweep": sweep,
+        "roofline": roofline, "roofline_prefill": roofline_prefill, "cpu_baseline": cpu, "sweep": sweep,
         "gpu": torch.cuda.get_device_name(dev),
     }
     print(json.dumps(line), flush=True)

@@ -44,14 +44,10 @@ DIRECT_MAX = int(os.environ.get("BLACKHOLE_HEX_DIRECT_MAX", "32"))      # slots 
 DEQUANT_MIN = int(os.environ.get("BLACKHOLE_HEX_DEQUANT_MIN", str(1 << 62)))
 PREFILL_MIN = 40     # slots per expert above which the fused path takes the 128-slot prefill kernels
 DECODE16_MAX = 12    # slots per expert up to which the decode kernels take 16-slot blocks
-# one launch per layer (plan, gate/up, down, sum) for one tier at 16-slot blocks and few slots;
-# opt-in: on MI355X it measured 91 us per config-2 T=16 layer against 72 us for the four launches
-LAYER = os.environ.get("BLACKHOLE_HEX_LAYER", "0") != "0"
 # a single tier's experts run as SPLIT parts on as many streams through the prefill kernels (see
 # hex_moe_fused); 1 or less keeps the tier whole. Two parts measured best: 433 / 439 / 447 us for
 # 2 / 3 / 4 parts at config 3, 1116 / 1136 / 1155 us at config 5 (T=2048).
 SPLIT = int(os.environ.get("BLACKHOLE_HEX_SPLIT", "2"))
-LAYER_MAX_SLOTS = 512
 
 
 def _n_in(p: dict, bits: int) -> int:
@@ -81,6 +77,7 @@ class HexTier:
     lookup: torch.Tensor | None = None
     _structs: dict = field(default_factory=dict, repr=False, compare=False)
     _experts_host: torch.Tensor | None = field(default=None, repr=False, compare=False)
+    _expert_set: frozenset = field(default=frozenset(), repr=False, compare=False)
     # the tier's SPLIT parts by expert (views of the same tensors), for hex_moe_fused's streams
     _parts: list | None = field(default=None, repr=False, compare=False)
     _is_part: bool = field(default=False, repr=False, compare=False)
@@ -104,6 +101,7 @@ class HexTier:
                 raise ValueError(f"{name}: {p['levels'].shape[-1]} levels for a {self.bits}-bit tier")
         dev = self.gate_proj["idx"].device
         self._experts_host = self.experts.detach().to("cpu", torch.int64)
+        self._expert_set = frozenset(self._experts_host.tolist())
         if self._experts_host.numel() and (int(self._experts_host.min()) < 0
                                            or int(self._experts_host.max()) >= num_experts):
             raise ValueError(f"tier expert ids must be in 0..{num_experts - 1}")
@@ -246,32 +244,67 @@ def default_config(slots: int, n_out: int, n_in: int, glu: bool, n_experts: int 
 
 # --------------------------------------------------------------------------- fused path
 
-_WORKSPACES: dict = {}
+# Workspaces of the decode kernels: int32 arrival counters, which must be zero when a call
+# starts and which every call leaves zero again, and float32 partial sums (no initial value).
+#  * One workspace per (device, stream, kind): calls that may overlap in time (tiers on side
+#    streams) never share one, and calls on one stream run in order.
+#  * A buffer handed to a kernel is never freed. A hipGraph captured with it replays into it
+#    for as long as the graph lives, so a workspace that has to grow takes new buffers and keeps
+#    the old ones alive (_RETIRED). Graphs captured on one stream share its workspace and are
+#    replayed in order, as a serving engine replays its graphs on one stream.
+#  * Counters are slices of a per-device arena zeroed once, outside any capture, so a captured
+#    call records no fill: every replay starts from the zeros the previous call left.
+_ARENA_INTS = 1 << 22            # int32 counters per arena (16 MiB)
+_SLICE_MIN = 1 << 16             # counters per workspace at least (so most never grow)
+_ARENAS: dict = {}               # device index -> [zeroed int32 tensor, ints handed out]
+_WORKSPACES: dict = {}           # (device index, stream, kind) -> (counters, partials)
+_RETIRED: list = []              # replaced buffers, kept alive for the graphs that use them
+
+
+def _zeroed_counters(device: torch.device, n: int) -> torch.Tensor:
+    """n int32 counters that are zero now, from the device's arena. Outside capture an arena
+    that is used up is replaced (its slices stay valid) and the host waits for its fill, so
+    streams other than the current one see zeros. Inside capture with the arena used up the
+    counters come from a captured fill (correct; the graph then replays one fill kernel)."""
+    ar = _ARENAS.get(device.index)
+    if ar is None or ar[0].numel() - ar[1] < n:
+        if torch.cuda.is_current_stream_capturing():
+            return torch.zeros(n, dtype=torch.int32, device=device)
+        if ar is not None:
+            _RETIRED.append(ar[0])
+        ar = _ARENAS[device.index] = [torch.zeros(max(n, _ARENA_INTS), dtype=torch.int32, device=device), 0]
+        torch.cuda.current_stream(device).synchronize()
+    t = ar[0][ar[1]:ar[1] + n]
+    ar[1] += -(-n // 64) * 64            # slices start on 256-byte boundaries
+    return t
+
+
+def _kept_workspace(kind: str, device: torch.device, n_counters: int, n_partials: int, min_partials: int):
+    """(counters, partials) of the current stream for workspace `kind`, grown (never freed) to at
+    least n_counters int32 and n_partials float32."""
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream, kind)
+    cnt, part = _WORKSPACES.get(key, (None, None))
+    if cnt is None or cnt.numel() < n_counters:
+        if cnt is not None:
+            _RETIRED.append(cnt)
+        cnt = _zeroed_counters(device, max(n_counters, _SLICE_MIN))
+    if part is None or part.numel() < n_partials:
+        if part is not None:
+            _RETIRED.append(part)
+        part = torch.empty(max(n_partials, min_partials), dtype=torch.float32, device=device)
+    _WORKSPACES[key] = (cnt, part)
+    return cnt, part
 
 
 def _workspace(device: torch.device, block_m: int, num_blocks: int, n_out: int, n_in: int, glu: bool):
-    """(counters, partials) for one fused launch on the current stream. The kernels leave the
-    int32 counters at zero, so both buffers are kept per (device, stream) and shared by every
-    call there (one stream runs its calls in order), grown when a call needs more. Inside graph
-    capture a missing or small workspace is allocated in the graph's pool (the counters zeroed
-    by a captured fill on every replay) and not kept."""
+    """(counters, partials) for one fused launch on the current stream (bh_hex_moe_workspace)."""
     lib = _lib.load()
     nc, npart = _lib.ctypes.c_int64(), _lib.ctypes.c_int64()
     _lib.check(lib.bh_hex_moe_workspace(num_blocks, n_out, n_in, block_m, int(glu), _lib.ctypes.byref(nc),
                                         _lib.ctypes.byref(npart)), "bh_hex_moe_workspace")
-    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
-    cnt, part = _WORKSPACES.get(key, (None, None))
-    keep = not torch.cuda.is_current_stream_capturing()
-    if cnt is None or cnt.numel() < nc.value:
-        cnt = torch.zeros(max(nc.value, 1 << 16), dtype=torch.int32, device=device)
-    if part is None or part.numel() < npart.value:
-        part = torch.empty(max(npart.value, 1 << 16), dtype=torch.float32, device=device)
-    if keep:
-        _WORKSPACES[key] = (cnt, part)
-    return cnt, part
+    return _kept_workspace("moe", device, nc.value, npart.value, 1 << 16)
 
 
-_LAYER_WORKSPACES: dict = {}
 _SIDE_STREAMS: dict = {}
 
 
@@ -282,50 +315,6 @@ def _side_stream(device: torch.device, i: int = 1) -> torch.cuda.Stream:
     if s is None:
         s = _SIDE_STREAMS[(device.index, i)] = torch.cuda.Stream(device)
     return s
-
-
-def _layer_workspace(device: torch.device, T: int, k: int, H: int, I: int, E: int):
-    """(counters, partials) of the one-launch layer kernel, kept per (device, stream) like
-    _workspace (the kernel leaves its counters at zero)."""
-    lib = _lib.load()
-    nc, npart = _lib.ctypes.c_int64(), _lib.ctypes.c_int64()
-    _lib.check(lib.bh_hex_moe_layer_workspace(T, k, H, I, E, _lib.ctypes.byref(nc), _lib.ctypes.byref(npart)),
-               "bh_hex_moe_layer_workspace")
-    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
-    cnt, part = _LAYER_WORKSPACES.get(key, (None, None))
-    keep = not torch.cuda.is_current_stream_capturing()
-    if cnt is None or cnt.numel() < nc.value:
-        cnt = torch.zeros(max(nc.value, 1 << 14), dtype=torch.int32, device=device)
-    if part is None or part.numel() < npart.value:
-        part = torch.empty(max(npart.value, 1 << 16), dtype=torch.float32, device=device)
-    if keep:
-        _LAYER_WORKSPACES[key] = (cnt, part)
-    return cnt, part
-
-
-def layer_wait_flag(device: torch.device | None = None) -> int:
-    """1 if a bounded wait of the layer kernel gave up on this device's current stream since its
-    workspace was made (the output of that call is invalid), else 0. Synchronises."""
-    device = device or torch.device("cuda", torch.cuda.current_device())
-    cnt, _ = _LAYER_WORKSPACES.get((device.index, torch.cuda.current_stream(device).cuda_stream), (None, None))
-    return 0 if cnt is None else int(cnt[32].item())
-
-
-def _launch_layer(x, w, flat_ids, t: HexTier, act, y, out, T: int, k: int) -> bool:
-    """The whole layer in one launch; False when the kernel does not take this shape."""
-    lib = _lib.load()
-    H, I, E = x.shape[1], act.shape[1], t.lookup.numel()
-    ids, code = _ids_arg(flat_ids)
-    cnt, part = _layer_workspace(x.device, T, k, H, I, E)
-    rc = lib.bh_hex_moe_layer(
-        x.data_ptr(), _lib.dtype_code(x.dtype), x.stride(0), ids.data_ptr(), code, w.data_ptr(), T, k,
-        t.struct("gate_proj"), t.struct("up_proj"), t.struct("down_proj"), t.bits, H, I, t.lookup.data_ptr(), E,
-        act.data_ptr(), act.stride(0), y.data_ptr(), y.stride(0), out.data_ptr(), out.stride(0),
-        cnt.data_ptr(), cnt.numel(), part.data_ptr(), part.numel(), _lib.stream_of(x))
-    if rc == _lib.ERR_UNSUPPORTED:
-        return False
-    _lib.check(rc, "bh_hex_moe_layer")
-    return True
 
 
 def _launch_glu(x, act, t: HexTier, sid, eid, npp, S, a_div, bm):
@@ -359,12 +348,12 @@ def _launch_down(act, y, t: HexTier, sid, eid, npp, S, w, bm):
 
 def _covers_all(tiers: list[HexTier]) -> bool:
     """Whether every expert id has a tier (then every slot's y row is written by a kernel)."""
-    seen = torch.zeros(tiers[0].lookup.numel(), dtype=torch.bool)
+    seen: set = set()
     for t in tiers:
         if t._experts_host is None:
             raise ValueError("HexTier.prepare(num_experts) has not been called")
-        seen[t._experts_host] = True
-    return bool(seen.all())
+        seen |= t._expert_set
+    return len(seen) == tiers[0].lookup.numel()
 
 
 def hex_moe_fused(x, topk_weights, topk_ids, tiers: list[HexTier], config: dict | None = None,
@@ -397,9 +386,6 @@ def hex_moe_fused(x, topk_weights, topk_ids, tiers: list[HexTier], config: dict 
     # reference's y (hex_moe.py:316), which halves the y traffic of the down kernel and the sum
     ydt = x.dtype if bm2 == 128 else torch.float32
     y = (torch.empty if _covers_all(tiers) else torch.zeros)(S, H, dtype=ydt, device=x.device)
-    if (LAYER and len(tiers) == 1 and bm1 == bm2 == 16 and S <= LAYER_MAX_SLOTS and align_mode == "auto"
-            and _launch_layer(x, w, flat, tiers[0], act, y, out, T, k)):
-        return out
 
     def run_tier(t: HexTier, lk: torch.Tensor | None) -> None:
         # one plan per tier when there are several, so each tier's launches walk only its blocks
@@ -516,6 +502,12 @@ def hex_moe(x: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor,
     if path not in ("auto", "fused", "dequant"):
         raise ValueError(f"unknown path {path!r}")
     capturing = x.is_cuda and torch.cuda.is_current_stream_capturing()
+    if capturing and (path == "dequant" or (path == "auto" and x.dtype == torch.float32)):
+        # the dequant path synchronises with the host (the routed experts are read back), which a
+        # capture cannot record; the fused kernels, the ones a graph can hold, take bf16/f16 only
+        raise NotImplementedError("the HEX dequant path cannot be captured in a graph: it reads the routed "
+                                  f"experts back to the host (activations {x.dtype}; capture bf16 or f16 "
+                                  "activations, which take the fused kernels)")
     if path == "dequant" or (path == "auto" and x.dtype == torch.float32) or (
             path == "auto" and config is None and not capturing and topk_ids.numel() >= DEQUANT_MIN):
         return hex_moe_dequant(x, topk_weights, topk_ids, tiers)

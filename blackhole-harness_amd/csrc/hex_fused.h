@@ -110,51 +110,64 @@ __device__ __forceinline__ void fields(const W& w, uint32_t r[4]) {
   transpose_rows4(r);
 }
 
+constexpr int kRsrcWord3 = 0x00020000;   // raw buffer, 32-bit data format (gfx9 family)
+constexpr int kCohere = 16;              // cache policy sc1: coherent across the device's L2s
+
+// Buffer offsets are unsigned 32-bit values. kOOR is a byte offset past every resource: a load
+// there returns zero and fetches nothing. Resources hold at most kMaxRecords bytes (the host
+// entry points refuse larger tensors). A load's offset is the sum of at most two terms, each
+// either kOOR or below kMaxRecords, plus an instruction offset below 4096: the sum stays below
+// 2^32, and it is out of range whenever one term is kOOR. So nothing wraps.
+constexpr uint32_t kOOR = 0x7FFF0000u;
+constexpr uint32_t kMaxRecords = kOOR;
+static_assert(kOOR >= kMaxRecords, "kOOR must lie past every resource");
+static_assert(2ull * kOOR + 4096ull < (1ull << 32), "offset sums must not wrap");
+
+// The signed VGPR offset the buffer builtins take, with the same 32 bits.
+__device__ __forceinline__ int voff(uint32_t v) { return __builtin_bit_cast(int, v); }
+
 // Raw buffer loads. They go through the compiler's buffer builtins, so the compiler tracks
 // each one and waits for exactly the loads a use needs. The whole byte offset goes in the
 // range-checked VGPR offset (soffset 0): an offset past the resource returns zero and fetches
 // nothing.
 template <int IMM>
-__device__ __forceinline__ void ld_x4(u32x4& d, __amdgpu_buffer_rsrc_t r, int v) {
-  d = __builtin_amdgcn_raw_buffer_load_b128(r, v + IMM, 0, 0);
+__device__ __forceinline__ void ld_x4(u32x4& d, __amdgpu_buffer_rsrc_t r, uint32_t v) {
+  d = __builtin_amdgcn_raw_buffer_load_b128(r, voff(v + IMM), 0, 0);
 }
 template <int IMM>
-__device__ __forceinline__ void ld_x3(u32x3& d, __amdgpu_buffer_rsrc_t r, int v) {
-  d = __builtin_amdgcn_raw_buffer_load_b96(r, v + IMM, 0, 0);
+__device__ __forceinline__ void ld_x3(u32x3& d, __amdgpu_buffer_rsrc_t r, uint32_t v) {
+  d = __builtin_amdgcn_raw_buffer_load_b96(r, voff(v + IMM), 0, 0);
 }
 template <int IMM>
-__device__ __forceinline__ void ld_x2(u32x2& d, __amdgpu_buffer_rsrc_t r, int v) {
-  d = __builtin_amdgcn_raw_buffer_load_b64(r, v + IMM, 0, 0);
+__device__ __forceinline__ void ld_x2(u32x2& d, __amdgpu_buffer_rsrc_t r, uint32_t v) {
+  d = __builtin_amdgcn_raw_buffer_load_b64(r, voff(v + IMM), 0, 0);
 }
 template <int IMM>
-__device__ __forceinline__ void ld_x1(uint32_t& d, __amdgpu_buffer_rsrc_t r, int v) {
-  d = __builtin_amdgcn_raw_buffer_load_b32(r, v + IMM, 0, 0);
+__device__ __forceinline__ void ld_x1(uint32_t& d, __amdgpu_buffer_rsrc_t r, uint32_t v) {
+  d = __builtin_amdgcn_raw_buffer_load_b32(r, voff(v + IMM), 0, 0);
 }
 template <int IMM>
-__device__ __forceinline__ void ld_u16(uint32_t& d, __amdgpu_buffer_rsrc_t r, int v) {
-  d = __builtin_amdgcn_raw_buffer_load_b16(r, v + IMM, 0, 0);
+__device__ __forceinline__ void ld_u16(uint32_t& d, __amdgpu_buffer_rsrc_t r, uint32_t v) {
+  d = __builtin_amdgcn_raw_buffer_load_b16(r, voff(v + IMM), 0, 0);
 }
 template <int IMM>
-__device__ __forceinline__ void ld_u8(uint32_t& d, __amdgpu_buffer_rsrc_t r, int v) {
-  d = __builtin_amdgcn_raw_buffer_load_b8(r, v + IMM, 0, 0);
+__device__ __forceinline__ void ld_u8(uint32_t& d, __amdgpu_buffer_rsrc_t r, uint32_t v) {
+  d = __builtin_amdgcn_raw_buffer_load_b8(r, voff(v + IMM), 0, 0);
 }
-
-constexpr int kRsrcWord3 = 0x00020000;   // raw buffer, 32-bit data format (gfx9 family)
-constexpr int kCohere = 16;              // cache policy sc1: coherent across the device's L2s
-constexpr int kOOR = 0x7FFF0000;         // byte offset past every resource: loads return zero, fetch nothing
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int64_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
-                                           (int)(bytes > 0x7FFFFFFF ? 0x7FFFFFFF : bytes), kRsrcWord3);
+                                           (int)(bytes > (int64_t)kMaxRecords ? (int64_t)kMaxRecords : bytes),
+                                           kRsrcWord3);
 }
 
 // Host side.
 int device_cus();
 constexpr int kGemmMt = 8;   // block_m / 16 of the prefill kernels (128-slot blocks)
 // Checks one projection for the fused kernels: scale blocks of 32 or 128 inputs (*sb = B / 32,
-// equal to a nonzero *sb on entry), 16-byte aligned 4-bit rows; clears *words when the scale
-// rows do not allow one load of a unit's scales.
-int proj_setup(const char* who, const bh_hex_proj* w, int bits, int64_t n_in, int* sb, int* words);
+// equal to a nonzero *sb on entry), 16-byte aligned 4-bit rows, each expert's matrix within one
+// buffer resource; clears *words when the scale rows do not allow one load of a unit's scales.
+int proj_setup(const char* who, const bh_hex_proj* w, int bits, int64_t n_out, int64_t n_in, int* sb, int* words);
 // Launches the prefill kernels for a plan of 128-slot blocks (no workspace).
 int gemm_run(const char* who, bool glu, int bits, int adt, int sb, const MoeArgs& a, int64_t num_blocks,
              hipStream_t stream);

@@ -126,18 +126,18 @@ __global__ __launch_bounds__(512, 2) void hex_gemm_kernel(MoeArgs a, int n_tiles
   // 16 (c / 4) + ln.
   const int x_rows = (int)((a.num_slots + a.a_div - 1) / a.a_div);
   const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(a.x, (int64_t)x_rows * a.s_xm * 2);
-  int xo[kMaxChunks];
+  uint32_t xo[kMaxChunks];
 #pragma unroll
   for (int i = 0; i < kChunks; ++i) {
     const int c = i * kGWaves + wave;
     const int s = slots[(c >> 2) * 16 + ln];
-    xo[i] = s < a.num_slots ? (int)((int64_t)(s / a.a_div) * a.s_xm * 2) + ((c & 3) * 32 + lg * 8) * 2 : kOOR;
+    xo[i] = s < a.num_slots ? (uint32_t)((int64_t)(s / a.a_div) * a.s_xm * 2) + ((c & 3) * 32 + lg * 8) * 2 : kOOR;
   }
   // Weights: the wave's groups of 16 rows; lane (ln, lg) reads block lg of the step of row ln.
   // Down: rows 256 nt + 16 (NG wave + g). GLU: group g is gate (g < NG/2) or up, half h = g % (NG/2):
   // rows 128 nt + 16 (NG/2 wave + h) of both, so a lane holds gate and up of the same outputs.
   constexpr int HG = kNG / 2;
-  int vw[kMaxNG], vb[kMaxNG];
+  uint32_t vw[kMaxNG], vb[kMaxNG];
   uint32_t cb[kMaxNG];
   __amdgpu_buffer_rsrc_t rw[kMaxNG], rb[kMaxNG];
 #pragma unroll
@@ -147,8 +147,8 @@ __global__ __launch_bounds__(512, 2) void hex_gemm_kernel(MoeArgs a, int n_tiles
     rw[g] = buffer_rsrc(w.idx + (int64_t)e * w.s_ie, (int64_t)a.N * w.s_in * 4);
     rb[g] = buffer_rsrc(w.block_scale + (int64_t)e * w.s_be, (int64_t)a.N * w.s_bn);
     const int n = GLU ? nt * 128 + (wave * HG + g % HG) * 16 + ln : nt * 256 + (wave * kNG + g) * 16 + ln;
-    vw[g] = n < a.N ? (int)((int64_t)n * w.s_in * 4) + lg * BLKB : kOOR;
-    vb[g] = n < a.N ? (int)((int64_t)n * w.s_bn) : kOOR;
+    vw[g] = n < a.N ? (uint32_t)((int64_t)n * w.s_in * 4) + lg * BLKB : kOOR;
+    vb[g] = n < a.N ? (uint32_t)((int64_t)n * w.s_bn) : kOOR;
     cb[g] = GLU ? (uint32_t)m * (TC * 2) + (lane & (TC / 2 - 1)) * 4u : (lane & (TC - 1)) * 4u;
   }
 
@@ -156,7 +156,7 @@ __global__ __launch_bounds__(512, 2) void hex_gemm_kernel(MoeArgs a, int n_tiles
   // i * waves + wave, 16 bytes per lane at lane * 16. Padding rows read out of range.
   auto load_a1 = [&](int st, int i, uint32_t* at) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)(at + (i * kGWaves + wave) * 256),
-                                             16, xo[i] + st * (kGK * 2), 0, 0, 0);
+                                             16, voff(xo[i] + st * (kGK * 2)), 0, 0, 0);
   };
   auto load_a = [&](int st, uint32_t* at) {
 #pragma unroll
@@ -417,7 +417,7 @@ int gemm_run(const char* who, bool glu, int bits, int adt, int sb, const MoeArgs
   const bh_hex_proj* ws[2] = {&a.w0, &a.w1};
   for (int m = 0; m < (glu ? 2 : 1); ++m) {
     const bh_hex_proj& w = *ws[m];
-    if ((int64_t)a.N * w.s_in * 4 > kOOR || (int64_t)a.N * w.s_bn > kOOR)
+    if ((int64_t)a.N * w.s_in * 4 > kMaxRecords || (int64_t)a.N * w.s_bn > kMaxRecords)
       return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": expert matrix over 2 GiB");
     if (sb == 1 && (w.s_bn % 4 || w.s_be % 4 || !aligned(w.block_scale, 4)))
       return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": block_m 128 with 32-input scale blocks needs "
@@ -427,7 +427,7 @@ int gemm_run(const char* who, bool glu, int bits, int adt, int sb, const MoeArgs
   if (a.s_om % ((glu || a.y16) ? 8 : 4) || !aligned(a.out, 16))
     return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": block_m 128 needs 16-byte aligned output rows");
   const int64_t x_rows = cdiv(a.num_slots, a.a_div);
-  if (x_rows * a.s_xm * 2 > kOOR) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": activations over 2 GiB");
+  if (x_rows * a.s_xm * 2 > kMaxRecords) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": activations over 2 GiB");
   const int64_t n_tiles = cdiv(a.N, glu ? gemm_cols<true>() : gemm_cols<false>());
   const int64_t wgs = num_blocks * n_tiles;
   if (wgs > INT32_MAX) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": plan too large");

@@ -4,8 +4,7 @@
 // Replaces the reference's _hex_moe_kernel (runtime/blackhole_runtime/hex_moe.py:109-151) in
 // both roles (GLU gate/up with SiLU, and down with the top-k weight) and the torch sum at
 // hex_moe.py:325. The decode-regime kernel is one persistent launch over the ranges of
-// hex_range.h, one range per workgroup; the 128-slot prefill kernels are in hex_gemm.hip and
-// the one-launch layer in hex_layer.hip.
+// hex_range.h, one range per workgroup; the 128-slot prefill kernels are in hex_gemm.hip.
 #include <string>
 
 #include "hex_range.h"
@@ -17,8 +16,7 @@ __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
   __shared__ MoeSmem<BITS, GLU, MT> sm;
   const Ranges rg = moe_ranges(a.npp[0] / (16 * MT), a.N, a.K, gridDim.x);
   if ((int64_t)blockIdx.x >= rg.G) return;
-  moe_range<BITS, ADT, GLU, MT, SB, KF, false>(a, sm, blockIdx.x, rg, a.lookup, a.sid, a.eid, LayerCtx{},
-                                               threadIdx.x);
+  moe_range<BITS, ADT, GLU, MT, SB, KF>(a, sm, blockIdx.x, rg, a.lookup, a.sid, a.eid, threadIdx.x);
 }
 
 // ----------------------------------------------------------------------------------- reduction
@@ -182,20 +180,23 @@ static int attach_workspace(const char* who, int32_t* counters, int64_t n_counte
   if (!counters || !partials || n_counters < w.counters || n_partials < w.partials)
     return fail(BH_HEX_ERR_VALUE, std::string(who) + ": workspace smaller than bh_hex_moe_workspace() asks");
   if (!aligned(partials, 16)) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": partials must be 16-byte aligned");
-  if (w.partials * 4 > 0x7FFFFFFF) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": plan too large");
+  if (w.partials * 4 > (int64_t)kMaxRecords) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": plan too large");
   a.counters = counters;
   a.part = partials;
   *grid = dim3((unsigned)moe_grid(num_blocks, n_out, n_in, mt));
   return BH_HEX_OK;
 }
 
-int proj_setup(const char* who, const bh_hex_proj* w, int bits, int64_t n_in, int* sb, int* words) {
+int proj_setup(const char* who, const bh_hex_proj* w, int bits, int64_t n_out, int64_t n_in, int* sb, int* words) {
   int block = 0;
   if (int rc = check_proj(w, n_in, who, &block)) return rc;
   if (block != 32 && block != 128)
     return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": fused kernels take scale blocks of 32 or 128 inputs");
   if (*sb && *sb != block / 32) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": gate and up scale blocks differ");
   *sb = block / 32;
+  // one expert's matrix is one buffer resource of at most kMaxRecords bytes
+  if (n_out * w->s_in * 4 > (int64_t)kMaxRecords || n_out * w->s_bn > (int64_t)kMaxRecords)
+    return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": expert matrix over 2 GiB");
   if (bits == 4 && (w->s_ie % 4 || w->s_in % 4 || !aligned(w->idx, 16)))
     return fail(BH_HEX_ERR_VALUE, std::string(who) + ": 4-bit idx rows must be 16-byte aligned");
   // a unit's scales in one load: 8 bytes at 32-input blocks, 2 bytes at 128-input blocks
@@ -220,12 +221,13 @@ extern "C" int bh_hex_moe_glu(const void* x, int32_t x_dtype, int64_t s_xm, void
   int rc = check_moe(who, bits, x_dtype, n_out, n_in, sorted_ids, expert_ids, num_blocks, npp, lookup, n_experts,
                      num_slots, tile, &mt, &sb, a);
   if (rc) return rc;
-  if ((rc = proj_setup(who, gate, bits, n_in, &sb, &words))) return rc;
-  if ((rc = proj_setup(who, up, bits, n_in, &sb, &words))) return rc;
+  if ((rc = proj_setup(who, gate, bits, n_out, n_in, &sb, &words))) return rc;
+  if ((rc = proj_setup(who, up, bits, n_out, n_in, &sb, &words))) return rc;
   if (a_div <= 0) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": a_div must be positive");
   if (!x || !act) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": null activation pointer");
   if (s_xm % 8 || !aligned(x, 16)) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": x rows must be 16-byte aligned");
-  if (cdiv(num_slots, a_div) * s_xm * 2 > 0x7FFFFFFF) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": x over 2 GiB");
+  if (cdiv(num_slots, a_div) * s_xm * 2 > (int64_t)kMaxRecords)
+    return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": x over 2 GiB");
   if (num_blocks == 0 || num_slots == 0) return BH_HEX_OK;
   a.x = reinterpret_cast<const uint16_t*>(x);
   a.s_xm = s_xm;
@@ -255,12 +257,13 @@ extern "C" int bh_hex_moe_down(const void* act, int32_t act_dtype, int64_t s_am,
   int rc = check_moe(who, bits, act_dtype, n_out, n_in, sorted_ids, expert_ids, num_blocks, npp, lookup, n_experts,
                      num_slots, tile, &mt, &sb, a);
   if (rc) return rc;
-  if ((rc = proj_setup(who, down, bits, n_in, &sb, &words))) return rc;
+  if ((rc = proj_setup(who, down, bits, n_out, n_in, &sb, &words))) return rc;
   if (!act || !y || !topk_w) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": null pointer");
   if (y_dtype != BH_HEX_F32 && y_dtype != act_dtype)
     return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": y dtype must be F32 or the activation dtype");
   if (s_am % 8 || !aligned(act, 16)) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": act rows must be 16-byte aligned");
-  if (num_slots * s_am * 2 > 0x7FFFFFFF) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": act over 2 GiB");
+  if (num_slots * s_am * 2 > (int64_t)kMaxRecords)
+    return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": act over 2 GiB");
   if (num_blocks == 0 || num_slots == 0) return BH_HEX_OK;
   a.x = reinterpret_cast<const uint16_t*>(act);
   a.s_xm = s_am;

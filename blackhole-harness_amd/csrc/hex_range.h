@@ -1,5 +1,5 @@
-// One range of work units of the decode-regime HEX expert GEMM, shared by the per-projection
-// kernels (hex_moe.hip) and the one-launch layer kernel (hex_layer.hip).
+// One range of work units of the decode-regime HEX expert GEMM (the per-projection kernels of
+// hex_moe.hip).
 //
 //  * Units of work are (expert block of the slot plan, 256-row tile, 256-input unit). A launch
 //    cuts them into G contiguous ranges [U g / G, U (g + 1) / G), one per workgroup turn, so
@@ -26,11 +26,6 @@
 //    (runtime/blackhole_runtime/hex_moe.py:109-151).
 // Weights therefore enter the matrix cores as round(level) and the block scale is applied to
 // the float32 block partial, where the reference rounds level * fp8 to the activation dtype.
-//
-// In the layer kernel (FUSED) a range also takes part in the hand-over between the phases: the
-// gate/up ranges count each finished item per plan block, a down range waits (bounded) for its
-// blocks' counts before it loads their activations, and at its end it counts its slots per
-// (token, row tile) and sums the tiles it completes over the token's k slots.
 #pragma once
 
 #include <type_traits>
@@ -57,7 +52,7 @@ template <int NM>
 struct ItemRes {
   __amdgpu_buffer_rsrc_t rw[NM];   // packed index words of the item's expert
   __amdgpu_buffer_rsrc_t rb[NM];   // its fp8 block scales
-  int vw[NM], vb[NM];              // lane offsets: row n, block lane / 16 of the unit
+  uint32_t vw[NM], vb[NM];         // lane offsets: row n, block lane / 16 of the unit
 };
 
 // The hot loop keeps every load unconditional and in a fixed order, so the compiler's waits
@@ -74,8 +69,6 @@ constexpr int kRows = 16 * kWaves;       // output rows of one work item: 16 per
 constexpr int kMinUnits = 2;             // units per workgroup below which the grid shrinks
                                          // (1 measured slower: config 2 at 1 token, 44.1 against
                                          // 40.5 us, the second unit's loads no longer hidden)
-constexpr int kMaxDone = 32;             // items one range of the layer kernel may finish
-constexpr int kSpinLimit = 1 << 20;      // polls of a bounded wait before it gives up
 
 // Units per trip P: the weight loads of P units are in flight per wave ahead of the math, and
 // the activation tiles of the next P units are fetched one trip ahead; one workgroup barrier
@@ -132,32 +125,10 @@ struct alignas(16) MoeSmem {
   int split_last[2];                     // this workgroup finishes split item k
 };
 
-// What the layer kernel adds to a range: device pointers (read from the kernel arguments where
-// they are used) and the layer kernel's shared memory.
-struct LayerPtrs {
-  int32_t* ready;       // per plan block: gate/up items finished
-  int32_t* tokcnt;      // per (token, down row tile): slots whose y rows are written
-  int32_t* flag;        // set to 1 when a bounded wait gives up
-  void* out;            // [T, N] in the activation dtype
-  int64_t s_ot;
-  int32_t k;            // slots per token
-  int32_t glu_tiles;    // gate/up row tiles per block
-};
-struct LayerCtx {
-  const LayerPtrs* p;
-  int* done;            // LDS: items this range finished, (block << 16) | row tile
-  int* comp;            // LDS: (token, row tile) pairs this range completed, t * nrt + pn
-  int* n_comp;          // LDS
-  int* n_done;          // LDS: entries of done (thread 0 keeps it)
-  const int* key;       // LDS: global expert of each covered slot, -1 for none
-  const int* tgt;       // LDS: covered slots of each token
-};
-
-// tid is threadIdx.x (the layer kernel passes a copy the compiler cannot hoist out of its loop).
-template <int BITS, int ADT, bool GLU, int MT, int SB, bool KF, bool FUSED>
+template <int BITS, int ADT, bool GLU, int MT, int SB, bool KF>
 __device__ __forceinline__ void moe_range(const MoeArgs& a, MoeSmem<BITS, GLU, MT>& sm, int64_t g, const Ranges& rg,
                                           const int* lut_src, const int32_t* plan_sid, const int32_t* plan_eid,
-                                          const LayerCtx& lc, const int tid) {
+                                          const int tid) {
   constexpr int L = 1 << BITS;
   constexpr int NPAIR = 1 << (2 * BITS);
   constexpr int NM = GLU ? 2 : 1;
@@ -195,8 +166,6 @@ __device__ __forceinline__ void moe_range(const MoeArgs& a, MoeSmem<BITS, GLU, M
   const int nblk = min((int)(item1 / nrt - pm0 + 1), MAXBLK);
 
   // ---- stage the plan: tier lookup, block experts, slot rows
-  if constexpr (FUSED)
-    if (tid == 0) *lc.n_done = 0;
   for (int i = tid; i < a.n_experts; i += kThreads) lut[i] = lut_src[i];
   for (int b = tid; b < MAXBLK; b += kThreads) blk_g[b] = b < nblk ? plan_eid[pm0 + b] : -1;
   for (int r = tid; r < MAXBLK * BM; r += kThreads)
@@ -239,8 +208,8 @@ __device__ __forceinline__ void moe_range(const MoeArgs& a, MoeSmem<BITS, GLU, M
       const bh_hex_proj& w = m == 0 ? a.w0 : a.w1;
       R.rw[m] = buffer_rsrc(w.idx + ee * w.s_ie, (int64_t)a.N * w.s_in * 4);
       R.rb[m] = buffer_rsrc(w.block_scale + ee * w.s_be, (int64_t)a.N * w.s_bn);
-      R.vw[m] = rv ? (int)(nrow * w.s_in * 4) + lg * BLKB : kOOR;
-      R.vb[m] = rv ? (int)(nrow * w.s_bn) : kOOR;
+      R.vw[m] = rv ? (uint32_t)(nrow * w.s_in * 4) + lg * BLKB : kOOR;
+      R.vb[m] = rv ? (uint32_t)(nrow * w.s_bn) : kOOR;
     }
   };
   // loads of unit s of the current descriptors; dummy units (past the range) read out of range.
@@ -249,11 +218,11 @@ __device__ __forceinline__ void moe_range(const MoeArgs& a, MoeSmem<BITS, GLU, M
   // invalid rows sit past every resource.
   auto load = [&](int s_, bool real, Stage<BITS, NM, SB, KF>& st) {
     const int s = __builtin_amdgcn_readfirstlane(real ? s_ : 0);
-    const int ws = real ? s * USTEP : kOOR;
-    const int bs = real ? (SB == 1 ? 8 : 2) * s : kOOR;
+    const uint32_t ws = real ? (uint32_t)(s * USTEP) : kOOR;
+    const uint32_t bs = real ? (uint32_t)((SB == 1 ? 8 : 2) * s) : kOOR;
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
-      const int vw = R.vw[m] + ws, vb = R.vb[m] + bs;
+      const uint32_t vw = R.vw[m] + ws, vb = R.vb[m] + bs;
       if constexpr (BITS == 4) {
         ld_x4<0>(st.w[m][0], R.rw[m], vw);
         ld_x4<4 * BLKB>(st.w[m][1], R.rw[m], vw);
@@ -279,59 +248,39 @@ __device__ __forceinline__ void moe_range(const MoeArgs& a, MoeSmem<BITS, GLU, M
     }
   };
 
-  // ---- layer kernel: a down range's blocks wait until their gate/up items are all written
-  // (bounded: past the limit the flag is raised and the range goes on)
-  auto wait_ready = [&](int64_t blk) {
-    if constexpr (FUSED && !GLU) {
-#pragma nounroll
-      for (int it = 0; __hip_atomic_load(lc.p->ready + blk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < lc.p->glu_tiles;
-           ++it) {
-        if (it >= kSpinLimit) {
-          __hip_atomic_store(lc.p->flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          break;
-        }
-        __builtin_amdgcn_s_sleep(4);
-      }
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);   // no activation load moves above the wait
-    }
-  };
-  // activations written by other workgroups of the same launch are read device-coherently
-  constexpr int XAUX = (FUSED && !GLU) ? kCohere : 0;
-
   // ---- activation stream: the tiles of the next trip, one dword per lane per (unit, step, subtile)
   const int x_rows = (int)((a.num_slots + a.a_div - 1) / a.a_div);
   const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(a.x, (int64_t)x_rows * a.s_xm * 2);
   // lane dword of a step's tile: wave w, lane l -> slot l / 4 of the subtile, inputs
   // 32 (w / 4) + 8 (w % 4) + 2 (l % 4) of the step (the fragment layout the MFMA reads)
   const int xcol = (wave >> 2) * 64 + (wave & 3) * 16 + (lane & 3) * 4;
-  int vx[MT];
+  uint32_t vx[MT];
   int ax_b = -1;
   auto act_rows = [&](int b) {
     const int e = expert_of(b);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {            // padding slots fetch nothing
       const int slot = slots[b * BM + mt * 16 + (lane >> 2)];
-      vx[mt] = (e >= 0 && slot < a.num_slots) ? (int)((int64_t)(slot / a.a_div) * a.s_xm * 2) + xcol : kOOR;
+      vx[mt] = (e >= 0 && slot < a.num_slots) ? (uint32_t)((int64_t)(slot / a.a_div) * a.s_xm * 2) + xcol : kOOR;
     }
   };
   uint32_t ax[P][2][MT];
   Pos ap{0, (int)(item0 - pm0 * nrt), (int)(ub - item0 * nun)};
   int ja = 0;
   auto act_trip = [&]() {                        // loads of the next P units' tiles
-    int xs[P][2], vxd[P][MT];
+    uint32_t xs[P][2], vxd[P][MT];
 #pragma unroll
     for (int d = 0; d < P; ++d) {
       const bool real = ja < n;
       const int b = min(ap.pm, MAXBLK - 1);
       if (real && b != ax_b) {
-        wait_ready(pm0 + b);
         act_rows(b);
         ax_b = b;
       }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) vxd[d][mt] = vx[mt];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) xs[d][h] = __builtin_amdgcn_readfirstlane(real ? (2 * ap.s + h) * 256 : kOOR);
+      for (int h = 0; h < 2; ++h) xs[d][h] = (uint32_t)__builtin_amdgcn_readfirstlane((int)(real ? (uint32_t)(2 * ap.s + h) * 256 : kOOR));
       advance(ap);
       ++ja;
     }
@@ -340,7 +289,7 @@ __device__ __forceinline__ void moe_range(const MoeArgs& a, MoeSmem<BITS, GLU, M
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) ax[d][h][mt] = __builtin_amdgcn_raw_buffer_load_b32(rx, vxd[d][mt] + xs[d][h], 0, XAUX);
+        for (int mt = 0; mt < MT; ++mt) ax[d][h][mt] = __builtin_amdgcn_raw_buffer_load_b32(rx, voff(vxd[d][mt] + xs[d][h]), 0, 0);
   };
 
   // ---- compute stream
@@ -439,9 +388,7 @@ __device__ __forceinline__ void moe_range(const MoeArgs& a, MoeSmem<BITS, GLU, M
     return min(min(slots[r0], slots[r0 + 1]), min(slots[r0 + 2], slots[r0 + 3])) < a.num_slots;
   };
 
-  // stores of one finished item (reference order: acc * es; silu(g) * (u * es_u); * topk weight).
-  // In the layer kernel they are device-coherent: other workgroups read them in this launch.
-  const __amdgpu_buffer_rsrc_t rout = buffer_rsrc(a.out, a.num_slots * a.s_om * (GLU ? 2 : 4));
+  // stores of one finished item (reference order: acc * es; silu(g) * (u * es_u); * topk weight)
   auto store_item = [&](const Pos& p, int b) {
     const int nrow = p.pn * kRows + wave * 16 + ln;
     if (nrow >= a.N) return;
@@ -457,31 +404,21 @@ __device__ __forceinline__ void moe_range(const MoeArgs& a, MoeSmem<BITS, GLU, M
         if constexpr (GLU) {
           const float gt = acc[mt][0][r] * es0;
           const float hv = gt / (1.0f + expf(-gt)) * (acc[mt][1][r] * es1);
-          if constexpr (FUSED)
-            __builtin_amdgcn_raw_buffer_store_b16((unsigned short)to_bits<ADT>(hv), rout, (int)(at * 2), 0, kCohere);
-          else
-            reinterpret_cast<uint16_t*>(a.out)[at] = (uint16_t)to_bits<ADT>(hv);
+          reinterpret_cast<uint16_t*>(a.out)[at] = (uint16_t)to_bits<ADT>(hv);
         } else {
           const float y = acc[mt][0][r] * es0 * slot_w[row];
-          if constexpr (FUSED)
-            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), rout, (int)(at * 4), 0, kCohere);
-          else if (a.y16)
+          if (a.y16)
             reinterpret_cast<uint16_t*>(a.out)[at] = (uint16_t)to_bits<ADT>(y);
           else
             reinterpret_cast<float*>(a.out)[at] = y;
         }
       }
   };
-  auto note_done = [&](const Pos& p, int b) {    // (layer kernel) items finished by this range
-    if constexpr (FUSED)
-      if (tid == 0) lc.done[(*lc.n_done)++] = (b << 16) | p.pn;
-  };
   Pos split_p0{0, 0, 0}, split_p1{0, 0, 0};
   int split_b0 = 0, split_b1 = 0, n_split = 0;
   auto end_item = [&](const Pos& p, int b, bool full, bool first) {
     if (full) {
       store_item(p, b);
-      note_done(p, b);
       return;
     }
     const __amdgpu_buffer_rsrc_t rp = buffer_rsrc(a.part, npart_floats * 4);
@@ -552,14 +489,12 @@ __device__ __forceinline__ void moe_range(const MoeArgs& a, MoeSmem<BITS, GLU, M
         }
       }
       store_item(p, b);
-      note_done(p, b);
     }
   };
 
   // ---- prologue: the rest of the staging (its waits leave nothing in flight), then the
   // pipeline's first loads in the loop's order: activation tiles, weights, and the first trip's
-  // tiles published. A down range of the layer kernel issues its weights first: they do not
-  // depend on the gate/up phase its activation loads may wait for.
+  // tiles published.
   for (int b = tid; b < MAXBLK; b += kThreads) {
     const int e = expert_of(b);
     blk_e[b] = e;
@@ -595,13 +530,10 @@ __device__ __forceinline__ void moe_range(const MoeArgs& a, MoeSmem<BITS, GLU, M
       ++jl;
     }
   };
-  constexpr bool kWeightsFirst = FUSED && !GLU;
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (kWeightsFirst) first_weights();
-  else act_trip();
+  act_trip();
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (kWeightsFirst) act_trip();
-  else first_weights();
+  first_weights();
   __builtin_amdgcn_sched_barrier(0);
   publish(ring[0]);
   __builtin_amdgcn_sched_barrier(0);
@@ -660,55 +592,6 @@ __device__ __forceinline__ void moe_range(const MoeArgs& a, MoeSmem<BITS, GLU, M
     __syncthreads();                   // the next trip's tiles are complete
   }
   finish_splits();
-  __builtin_amdgcn_s_waitcnt(0);       // no load of this wave is left in flight; its stores are done
-
-  if constexpr (FUSED) {
-    // hand-over: every wave's stores of this range are complete before any count moves
-    if constexpr (!GLU)
-      if (tid == 0) *lc.n_comp = 0;
-    __syncthreads();
-    const int n_done = *lc.n_done;
-    if constexpr (GLU) {
-      for (int i = tid; i < n_done; i += kThreads)
-        __hip_atomic_fetch_add(lc.p->ready + pm0 + (lc.done[i] >> 16), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    } else {
-      // count the finished items' slots per (token, row tile); the last arrival of a pair sums it
-      for (int q = tid; q < n_done * BM; q += kThreads) {
-        const int i = q / BM, r = q % BM;
-        const int b = lc.done[i] >> 16, pn = lc.done[i] & 0xFFFF;
-        const int slot = slots[b * BM + r];
-        if (slot < a.num_slots) {
-          const int tok = slot / lc.p->k;
-          int32_t* c = lc.p->tokcnt + (int64_t)tok * nrt + pn;
-          const int old = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          if (old == lc.tgt[tok] - 1) {
-            __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            lc.comp[atomicAdd(lc.n_comp, 1)] = tok * nrt + pn;
-          }
-        }
-      }
-      __syncthreads();
-      // out[t, tile] = sum over the token's covered slots in slot order, in float32, rounded once
-      const int nc = *lc.n_comp;
-      for (int c = wave; c < nc; c += kWaves) {
-        const int tok = lc.comp[c] / nrt, pn = lc.comp[c] % nrt;
-        const int col = pn * kRows + lane * 4;
-        if (col >= a.N) continue;
-        f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
-        const int kk = lc.p->k;
-        for (int j = 0; j < kk; ++j) {
-          const int slot = tok * kk + j;
-          if (lc.key[slot] < 0) continue;
-          s4 += __builtin_bit_cast(
-              f32x4, __builtin_amdgcn_raw_buffer_load_b128(rout, (int)(((int64_t)slot * a.s_om + col) * 4), 0, kCohere));
-        }
-        u32x2 v;
-        v[0] = to_bits<ADT>(s4[0]) | (to_bits<ADT>(s4[1]) << 16);
-        v[1] = to_bits<ADT>(s4[2]) | (to_bits<ADT>(s4[3]) << 16);
-        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(lc.p->out) + tok * lc.p->s_ot + col) = v;
-      }
-    }
-  }
 }
 
 }  // namespace bh

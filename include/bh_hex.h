@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define BH_HEX_ABI_VERSION 6
+#define BH_HEX_ABI_VERSION 7
 
 enum bh_hex_status {
   BH_HEX_OK = 0,
@@ -182,34 +182,6 @@ int bh_hex_moe_workspace(int64_t num_blocks, int64_t n_out, int64_t n_in, int32_
 int bh_hex_moe_reduce(const void* y, int32_t y_dtype, int64_t s_ym, const void* topk_ids, int32_t ids_dtype,
                       int32_t n_experts, int64_t T, int32_t k, int64_t H, void* out, int32_t out_dtype, int64_t s_ot,
                       void* stream);
-
-/* A whole decode-regime layer over one tier in one launch: the slot plan, the gate/up half, the
- * down half and the k-slot sum, with the numerics of bh_hex_moe_glu, bh_hex_moe_down and
- * bh_hex_moe_reduce (its slot plan uses 16-slot blocks; slots whose id is outside
- * [0, n_experts) or whose expert has no tier entry add nothing):
- *   out[t] = sum_j down(silu(gate(x[t])) * up(x[t]))[slot t k + j] * topk_w[t k + j].
- * x [T, H] and out [T, H] are BF16 or F16 (x_dtype); topk_ids [T, k] (I32 or I64) and
- * topk_w [T, k] float are contiguous; act [T k, I] (x dtype) and y [T k, H] float are scratch.
- * T k at most 512 and floor(T k / 16) + min(n_experts, T k) at most 320; H and I multiples of
- * 256; gate, up and down with the same scale block and scale rows aligned for one load per 256
- * inputs. Other shapes return BH_HEX_ERR_UNSUPPORTED (the caller then takes the per-projection
- * entry points). The workspace comes from bh_hex_moe_layer_workspace: its counters must be zero
- * before the first call and are left zero by every call except counters[32], which a call sets
- * to 1 if one of its bounded waits gave up (its output is then invalid; no such wait gives up
- * unless the device stops scheduling the launch's workgroups). Calls sharing a workspace must
- * not overlap. Replaces the launches of hex_moe_fused (hex_moe.py:304-325) for one tier:
- * align (201-222), _hex_moe_kernel twice (322, 324) and y.view(T, k, H).sum(1) (325). */
-int bh_hex_moe_layer(const void* x, int32_t x_dtype, int64_t s_xm, const void* topk_ids, int32_t ids_dtype,
-                     const float* topk_w, int64_t T, int32_t k, const bh_hex_proj* gate, const bh_hex_proj* up,
-                     const bh_hex_proj* down, int32_t bits, int64_t H, int64_t I, const int32_t* lookup,
-                     int32_t n_experts, void* act, int64_t s_am, float* y, int64_t s_ym, void* out, int64_t s_ot,
-                     int32_t* counters, int64_t n_counters, float* partials, int64_t n_partials, void* stream);
-
-/* Workspace of bh_hex_moe_layer on the current device: *n_counters int32 (zero before first
- * use) and *n_partials floats (16-byte aligned, no initial value). No counterpart in the
- * reference. */
-int bh_hex_moe_layer_workspace(int64_t T, int32_t k, int64_t H, int64_t I, int32_t n_experts, int64_t* n_counters,
-                               int64_t* n_partials);
 
 #ifdef __cplusplus
 }

@@ -140,33 +140,3 @@ def test_check_maps_status_to_reference_exceptions():
         _lib.check(_lib.ERR_UNSUPPORTED, "x")
     with pytest.raises(RuntimeError):
         _lib.check(_lib.ERR_HIP, "x")
-
-
-def _layer_ws(lib, *args):
-    nc, npart = ctypes.c_int64(), ctypes.c_int64()
-    rc = lib.bh_hex_moe_layer_workspace(*args, ctypes.byref(nc), ctypes.byref(npart))
-    return rc, nc.value, npart.value
-
-
-def test_layer_workspace_and_host_side_errors():
-    """bh_hex_moe_layer's workspace grows with the batch; shapes the one-launch kernel does not
-    take are refused as unsupported (the Python layer then takes the per-projection launches),
-    before anything reaches the device."""
-    lib = _lib.load()
-    assert _layer_ws(lib, -1, 8, 2048, 768, 96)[0] == _lib.ERR_VALUE
-    rc, nc, npart = _layer_ws(lib, 16, 8, 2048, 768, 96)
-    assert rc == _lib.OK and nc > 64 + 320 and npart > 0
-    rc, nc2, npart2 = _layer_ws(lib, 64, 8, 2048, 768, 96)
-    assert rc == _lib.OK and nc2 > nc and npart2 == npart
-    w = _lib.HexProj(16, 16, 16, 16, 0, 0, 0, 0, 128)     # scale rows of 0 bytes: never loaded here
-
-    def call(T=16, k=8, H=2048, I=768, E=96, xdt=_lib.BF16, bits=4, cnt=None, ncnt=0):
-        return lib.bh_hex_moe_layer(16, xdt, H, 16, _lib.I64, 16, T, k, ctypes.byref(w), ctypes.byref(w),
-                                    ctypes.byref(w), bits, H, I, 16, E, 16, I, 16, H, 16, H, cnt, ncnt, 16, 1 << 30,
-                                    None)
-    _status(call(bits=5), _lib.ERR_UNSUPPORTED, "bits")
-    _status(call(xdt=_lib.F32), _lib.ERR_UNSUPPORTED, "BF16 or F16")
-    _status(call(T=100), _lib.ERR_UNSUPPORTED, "512")                      # 800 slots
-    _status(call(T=64, E=1000), _lib.ERR_UNSUPPORTED, "512")               # 32 + 512 blocks
-    _status(call(I=640), _lib.ERR_UNSUPPORTED, "multiples of 256")
-    _status(call(), _lib.ERR_VALUE, "workspace")

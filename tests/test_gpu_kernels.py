@@ -450,140 +450,85 @@ def test_three_tiers_on_three_streams():
             torch.cuda.synchronize()
 
 
-# --------------------------------------------------------------------------- one-launch layer
+# --------------------------------------------------------------------------- workspaces
 
 
-def _inputs(T, E, k, H, dt, seed, skew=False):
-    w, ids = routing(T, E, k, seed=seed, skew=skew)
-    x = torch.from_numpy(np.random.default_rng(seed + 1).standard_normal((T, H)).astype(np.float32)).to(dt)
-    return x, w, ids
+def _ws_key(stream, kind="moe"):
+    return (torch.device(DEV).index or 0, stream.cuda_stream, kind)
 
 
-def run_layer(tier, x, w, ids):
-    """bh_hex_moe_layer directly (asserting that it takes the shape) -> out [T, H]."""
-    T, k = ids.shape
-    H, I = x.shape[1], tier.gate_proj["idx"].shape[1]
-    act = torch.empty(T * k, I, dtype=x.dtype, device=DEV)
-    y = torch.empty(T * k, H, dtype=torch.float32, device=DEV)
-    out = torch.empty(T, H, dtype=x.dtype, device=DEV)
-    assert hm._launch_layer(x, w.reshape(-1).float().contiguous(), ids.reshape(-1), tier, act, y, out, T, k)
-    return out
+def test_capture_records_no_fill(monkeypatch):
+    """A decode layer captured on a stream that never ran it eagerly: its workspace counters
+    come from the zeroed arena, so the capture calls no torch.zeros (no fill kernel replays with
+    the layer), and every replay equals the eager result."""
+    say("capture records no fill")
+    E, H, I, k, T = 16, 512, 256, 4, 24
+    ref, tiers = make_layer(E, H, I, 0, (4,), seed=60, block=128)
+    w, ids = routing(T, E, k, seed=60)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(60)).to(torch.bfloat16).to(DEV)
+    wd, idd = torch.from_numpy(w).to(DEV), torch.from_numpy(ids).to(DEV)
+    eager = hm.hex_moe_fused(x, wd, idd, tiers)
+    want = O.moe_reference(x.float().cpu().numpy(), w, ids, ref, "bf16")
+    assert O.rel_err(eager.float().cpu().numpy(), want) < TOL_16
+    torch.cuda.synchronize()
 
-
-def per_projection(tiers, x, w, ids):
-    """The four launches over each whole tier (no split into expert halves), as the one-launch
-    layer kernel runs them."""
-    old = hm.LAYER, hm.SPLIT
-    try:
-        hm.LAYER, hm.SPLIT = False, False
-        return hm.hex_moe_fused(x, w, ids, tiers)
-    finally:
-        hm.LAYER, hm.SPLIT = old
-
-
-@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("block", [32, 128])
-@pytest.mark.parametrize("bits", [3, 4])
-def test_layer_kernel(bits, block, dt):
-    """The one-launch layer against the oracle (1e-2) and against the per-projection launches,
-    from one slot to 512; each batch twice, so every counter must have been left at zero. (The
-    per-projection launches size their grid from the plan's upper bound, so their ranges, and
-    with them the float32 association of split items, can differ: close, not bit-equal.)"""
-    say(f"layer kernel bits={bits} block={block} {dt}")
-    E, H, I, k = 16, 512, 256, 4
-    ref, tiers = make_layer(E, H, I, 0, (bits,), seed=41, block=block)
-    act_round = {torch.bfloat16: "bf16", torch.float16: "f16"}[dt]
-    for T in (1, 7, 16, 128):
-        x, w, ids = _inputs(T, E, k, H, dt, seed=T, skew=T == 128)
-        want = O.moe_reference(x.float().numpy(), w, ids, ref, act_round)
-        xd, wd, idd = x.to(DEV), torch.from_numpy(w).to(DEV), torch.from_numpy(ids).to(DEV)
-        base = per_projection(tiers, xd, wd, idd)
-        for rep in range(2):
-            got = run_layer(tiers[0], xd, wd, idd)
-            assert O.rel_err(got.float().cpu().numpy(), want) < TOL_16, (T, rep)
-            assert O.rel_err(got.float().cpu().numpy(), base.float().cpu().numpy()) < TOL_16, (T, rep)
-    assert hm.layer_wait_flag() == 0
-
-
-def test_layer_kernel_benchmark_shape():
-    """Config 2's layer (E=96, H=2048, I=768, top-8, 4-bit, 128-input scales) at T=16 and 64:
-    gate/up items one per workgroup, down items split between workgroups. Both paths launch 256
-    workgroups here, so their ranges agree and the results are bit-equal."""
-    say("layer kernel, benchmark shape")
-    E, H, I, k = 96, 2048, 768, 8
-    ref, tiers = make_layer(E, H, I, 0, (4,), seed=42, block=128)
-    for T in (16, 64):
-        x, w, ids = _inputs(T, E, k, H, torch.bfloat16, seed=T)
-        xd, wd, idd = x.to(DEV), torch.from_numpy(w).to(DEV), torch.from_numpy(ids).to(DEV)
-        got = run_layer(tiers[0], xd, wd, idd)
-        assert torch.equal(got, per_projection(tiers, xd, wd, idd)), T
-        want = O.moe_reference(x.float().numpy(), w, ids, ref, "bf16")
-        assert O.rel_err(got.float().cpu().numpy(), want) < TOL_16, T
-    assert hm.layer_wait_flag() == 0
-
-
-def test_layer_kernel_uncovered_and_invalid_ids():
-    """A tier with a quarter of the experts: slots of the others, and ids outside [0, E), add
-    nothing; tokens with no covered slot get zero rows."""
-    say("layer kernel, uncovered experts and invalid ids")
-    E, H, I, k, T = 16, 256, 256, 2, 40
-    ref, tiers = make_layer(E, H, I, 4, (4, 3), seed=43)
-    ref, tiers = ref[:1], tiers[:1]
-    x, w, ids = _inputs(T, E, k, H, torch.bfloat16, seed=9)
-    ids[0, 0], ids[5, 1], ids[7, 0] = -1, E, E + 100
-    want = O.moe_reference(x.float().numpy(), w, ids, ref, "bf16")
-    got = run_layer(tiers[0], x.to(DEV), torch.from_numpy(w).to(DEV), torch.from_numpy(ids).to(DEV))
-    assert O.rel_err(got.float().cpu().numpy(), want) < TOL_16
-    covered = set(np.asarray(ref[0]["experts"]).tolist())
-    empty = [t for t in range(T) if not any(int(e) in covered for e in ids[t])]
-    assert empty and torch.count_nonzero(got[empty]).item() == 0
-    assert hm.layer_wait_flag() == 0
-
-
-def test_layer_kernel_shapes_it_does_not_take():
-    """Widths that are not multiples of 256, more than 512 slots, or several tiers: the fused path
-    falls back to the per-projection launches."""
-    say("layer kernel, shapes it does not take")
-    E, H, I, k = 8, 256, 128, 2
-    ref, tiers = make_layer(E, H, I, 0, (4,), seed=44)
-    x, w, ids = _inputs(4, E, k, H, torch.bfloat16, seed=1)
-    xd, wd, idd = x.to(DEV), torch.from_numpy(w).to(DEV), torch.from_numpy(ids).to(DEV)
-    act = torch.empty(8, I, dtype=torch.bfloat16, device=DEV)
-    y = torch.empty(8, H, device=DEV)
-    out = torch.empty(4, H, dtype=torch.bfloat16, device=DEV)
-    assert not hm._launch_layer(xd, wd.reshape(-1), idd.reshape(-1), tiers[0], act, y, out, 4, k)
-    assert run_fused(ref, tiers, 4, E, k, H, seed=1) < TOL_16
-    E, H, I = 16, 256, 256
-    ref, tiers = make_layer(E, H, I, 0, (4,), seed=45)
-    assert run_fused(ref, tiers, 300, E, k, H, seed=2) < TOL_16          # 600 slots
-
-
-def test_layer_kernel_graph_capture():
-    """The one-launch layer captured in a hipGraph, replayed with eager layers in between; every
-    replay equals the eager result."""
-    say("layer kernel, graph capture")
-    E, H, I, k, T = 16, 512, 256, 4, 16
-    ref, tiers = make_layer(E, H, I, 0, (4,), seed=46, block=128)
-    x, w, ids = _inputs(T, E, k, H, torch.bfloat16, seed=3)
-    xd, wd, idd = x.to(DEV), torch.from_numpy(w).to(DEV), torch.from_numpy(ids).to(DEV)
-    eager = run_layer(tiers[0], xd, wd, idd)
-    old = hm.LAYER
-    try:
-        hm.LAYER = True                          # the one-launch layer is opt-in
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            hm.hex_moe_fused(xd, wd, idd, tiers)
-        torch.cuda.current_stream().wait_stream(s)
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            out = hm.hex_moe_fused(xd, wd, idd, tiers)
-    finally:
-        hm.LAYER = old
+    def no_zeros(*a, **kw):
+        raise AssertionError("torch.zeros called while capturing the layer")
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    assert _ws_key(s) not in hm._WORKSPACES
+    with torch.cuda.graph(g, stream=s):
+        monkeypatch.setattr(torch, "zeros", no_zeros)
+        try:
+            out = hm.hex_moe_fused(x, wd, idd, tiers)
+        finally:
+            monkeypatch.undo()
+    assert _ws_key(s) in hm._WORKSPACES
     for i in range(3):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager), i
-        _ = run_layer(tiers[0], xd * 2, wd, idd)             # unrelated eager work between replays
+        _ = hm.hex_moe_fused(x * 2, wd, idd, tiers)
         torch.cuda.synchronize()
-    assert hm.layer_wait_flag() == 0
+
+
+def test_workspace_kept_alive_when_it_grows():
+    """Warm-up and capture on one stream, then an eager call on that stream whose workspace must
+    grow: the graph's buffers stay allocated (nothing else is given their memory), and replays
+    still equal the eager result."""
+    say("workspace kept alive when it grows")
+    E, H, I, k = 16, 512, 256, 4
+    ref, tiers = make_layer(E, H, I, 0, (4,), seed=61, block=128)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+
+    def inputs(T, seed):
+        w, ids = routing(T, E, k, seed=seed)
+        x = torch.randn(T, H, generator=torch.Generator().manual_seed(seed)).to(torch.bfloat16).to(DEV)
+        return x, torch.from_numpy(w).to(DEV), torch.from_numpy(ids).to(DEV)
+    xs, ws_, ids_s = inputs(2, 61)          # 8 slots: a small workspace
+    xb, wb, idb = inputs(64, 62)            # 256 slots on 32-slot blocks: a larger one
+    with torch.cuda.stream(s):
+        eager = hm.hex_moe_fused(xs, ws_, ids_s, tiers)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        out = hm.hex_moe_fused(xs, ws_, ids_s, tiers)
+    torch.cuda.synchronize()
+    before = [t.data_ptr() for t in hm._WORKSPACES[_ws_key(s)]]
+    with torch.cuda.stream(s):
+        big = hm.hex_moe_fused(xb, wb, idb, tiers)
+    torch.cuda.synchronize()
+    after = [t.data_ptr() for t in hm._WORKSPACES[_ws_key(s)]]
+    assert after[1] != before[1], "the partials did not grow: the test does not exercise growth"
+    kept = {t.data_ptr() for t in hm._RETIRED}
+    assert before[1] in kept
+    # fresh allocations with other contents: none may take the graph's old workspace
+    junk = [torch.full((1 << 20,), 7, dtype=torch.int32, device=DEV) for _ in range(8)]
+    _, idsb_np = routing(64, E, k, seed=62)
+    want_big = O.moe_reference(xb.float().cpu().numpy(), wb.cpu().numpy(), idsb_np, ref, "bf16")
+    assert O.rel_err(big.float().cpu().numpy(), want_big) < TOL_16
+    for i in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), i
+    del junk

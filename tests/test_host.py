@@ -102,6 +102,25 @@ def test_kernels_refuse_cpu_tensors():
         hm.hex_moe(x, torch.ones(2, 1), torch.zeros(2, 1, dtype=torch.long), [t], path="triton")
 
 
+def test_dequant_path_refused_while_capturing(monkeypatch):
+    """Under graph capture, float32 activations (path "auto") and path "dequant" raise a clear
+    NotImplementedError instead of reaching the host synchronisation of the dequant path; bf16
+    activations go on to the fused path (which then refuses the CPU tensor here)."""
+    class FakeX:                     # a device tensor as far as hex_moe's dispatch looks
+        is_cuda = True
+        dtype = torch.float32
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    t = _tier([0, 1], 4).prepare(2)
+    ids = torch.zeros(2, 1, dtype=torch.long)
+    with pytest.raises(NotImplementedError, match="cannot be captured"):
+        hm.hex_moe(FakeX(), torch.ones(2, 1), ids, [t])
+    FakeX.dtype = torch.bfloat16
+    with pytest.raises(NotImplementedError, match="cannot be captured"):
+        hm.hex_moe(FakeX(), torch.ones(2, 1), ids, [t], path="dequant")
+    with pytest.raises(ValueError, match="GPU"):
+        hm.hex_moe(torch.zeros(2, 64, dtype=torch.bfloat16), torch.ones(2, 1), ids, [t])
+
+
 # --------------------------------------------------------------------------- the vLLM plugin
 
 
