@@ -48,6 +48,9 @@ DECODE16_MAX = 12    # slots per expert up to which the decode kernels take 16-s
 # hex_moe_fused); 1 or less keeps the tier whole. Two parts measured best: 433 / 439 / 447 us for
 # 2 / 3 / 4 parts at config 3, 1116 / 1136 / 1155 us at config 5 (T=2048).
 SPLIT = int(os.environ.get("BLACKHOLE_HEX_SPLIT", "2"))
+# slots up to which the decode kernels sort the slots by expert themselves (bh_hex_moe_*_ids), so
+# no align launch precedes them (at most 1024; 0 always launches the align kernel)
+KERNEL_PLAN_MAX = min(1024, int(os.environ.get("BLACKHOLE_HEX_KERNEL_PLAN_MAX", "1024")))
 
 
 def _n_in(p: dict, bits: int) -> int:
@@ -331,6 +334,22 @@ def _launch_glu(x, act, t: HexTier, sid, eid, npp, S, a_div, bm):
         tile, cnt.data_ptr(), cnt.numel(), part.data_ptr(), part.numel(), _lib.stream_of(x)), "bh_hex_moe_glu")
 
 
+def _launch_glu_ids(x, act, t: HexTier, ids, code, S, a_div, bm):
+    """The gate/up launch that sorts the slots itself (no align launch before it)."""
+    lib = _lib.load()
+    n_out = t.gate_proj["idx"].shape[1]
+    n_in = _n_in(t.gate_proj, t.bits)
+    assert x.shape[1] == n_in, f"input width {x.shape[1]} != HEX width {n_in}"
+    tile = _lib.HexTile(bm, 256, 1)
+    E = t.lookup.numel()
+    cnt, part = _workspace(x.device, bm, lib.bh_hex_align_max_blocks(S, E, bm), n_out, n_in, True)
+    _lib.check(lib.bh_hex_moe_glu_ids(
+        x.data_ptr(), _lib.dtype_code(x.dtype), x.stride(0), act.data_ptr(), act.stride(0),
+        t.struct("gate_proj"), t.struct("up_proj"), t.bits, n_out, n_in, ids.data_ptr(), code, t.lookup.data_ptr(), E,
+        S, a_div, tile, cnt.data_ptr(), cnt.numel(), part.data_ptr(), part.numel(), _lib.stream_of(x)),
+        "bh_hex_moe_glu_ids")
+
+
 def _launch_down(act, y, t: HexTier, sid, eid, npp, S, w, bm):
     lib = _lib.load()
     n_out = t.down_proj["idx"].shape[1]
@@ -344,6 +363,21 @@ def _launch_down(act, y, t: HexTier, sid, eid, npp, S, w, bm):
         sid.data_ptr(), eid.data_ptr(), eid.numel(), npp.data_ptr(), t.lookup.data_ptr(), t.lookup.numel(), S,
         w.data_ptr(), tile, cnt.data_ptr(), cnt.numel(), part.data_ptr(), part.numel(), _lib.stream_of(act)),
         "bh_hex_moe_down")
+
+
+def _launch_down_ids(act, y, t: HexTier, ids, code, S, w, bm):
+    """The down launch that sorts the slots itself."""
+    lib = _lib.load()
+    n_out = t.down_proj["idx"].shape[1]
+    n_in = _n_in(t.down_proj, t.bits)
+    assert act.shape[1] == n_in, f"input width {act.shape[1]} != HEX width {n_in}"
+    tile = _lib.HexTile(bm, 256, 1)
+    E = t.lookup.numel()
+    cnt, part = _workspace(act.device, bm, lib.bh_hex_align_max_blocks(S, E, bm), n_out, n_in, False)
+    _lib.check(lib.bh_hex_moe_down_ids(
+        act.data_ptr(), _lib.dtype_code(act.dtype), act.stride(0), y.data_ptr(), _lib.dtype_code(y.dtype), y.stride(0),
+        t.struct("down_proj"), t.bits, n_out, n_in, ids.data_ptr(), code, t.lookup.data_ptr(), E, S, w.data_ptr(),
+        tile, cnt.data_ptr(), cnt.numel(), part.data_ptr(), part.numel(), _lib.stream_of(act)), "bh_hex_moe_down_ids")
 
 
 def _covers_all(tiers: list[HexTier]) -> bool:
@@ -387,12 +421,24 @@ def hex_moe_fused(x, topk_weights, topk_ids, tiers: list[HexTier], config: dict 
     ydt = x.dtype if bm2 == 128 else torch.float32
     y = (torch.empty if _covers_all(tiers) else torch.zeros)(S, H, dtype=ydt, device=x.device)
 
+    # at most KERNEL_PLAN_MAX slots the decode kernels sort the slots themselves (with the tier's
+    # lookup, so each tier's launches walk only its blocks) and no align launch precedes them
+    ids_flat, ids_code = _ids_arg(flat)
+    own1 = align_mode == "auto" and bm1 != 128 and S <= KERNEL_PLAN_MAX
+    own2 = align_mode == "auto" and bm2 != 128 and S <= KERNEL_PLAN_MAX
+
     def run_tier(t: HexTier, lk: torch.Tensor | None) -> None:
         # one plan per tier when there are several, so each tier's launches walk only its blocks
-        p1 = plan(flat, E, bm1, align_mode, lk)
-        p2 = p1 if bm2 == bm1 else plan(flat, E, bm2, align_mode, lk)
-        _launch_glu(x, act, t, *p1, S, k, bm1)
-        _launch_down(act, y, t, *p2, S, w, bm2)
+        p1 = None if own1 else plan(flat, E, bm1, align_mode, lk)
+        p2 = None if own2 else (p1 if (bm2 == bm1 and p1 is not None) else plan(flat, E, bm2, align_mode, lk))
+        if own1:
+            _launch_glu_ids(x, act, t, ids_flat, ids_code, S, k, bm1)
+        else:
+            _launch_glu(x, act, t, *p1, S, k, bm1)
+        if own2:
+            _launch_down_ids(act, y, t, ids_flat, ids_code, S, w, bm2)
+        else:
+            _launch_down(act, y, t, *p2, S, w, bm2)
 
     # Each slot is served by one tier, so the tiers write disjoint rows of act and y: each later
     # tier runs on a side stream of its own beside the first (each stream keeps its own
@@ -417,9 +463,8 @@ def hex_moe_fused(x, topk_weights, topk_ids, tiers: list[HexTier], config: dict 
         run_tier(chains[0], chains[0].lookup)
         for side in sides:
             main.wait_stream(side)
-    ids, code = _ids_arg(flat)
     lib = _lib.load()
-    _lib.check(lib.bh_hex_moe_reduce(y.data_ptr(), _lib.dtype_code(y.dtype), y.stride(0), ids.data_ptr(), code, E, T, k,
+    _lib.check(lib.bh_hex_moe_reduce(y.data_ptr(), _lib.dtype_code(y.dtype), y.stride(0), ids_flat.data_ptr(), ids_code, E, T, k,
                                      H, out.data_ptr(), _lib.dtype_code(out.dtype), out.stride(0), _lib.stream_of(x)),
                "bh_hex_moe_reduce")
     return out

@@ -101,6 +101,49 @@ __device__ __forceinline__ void transpose_rows4(uint32_t r[4]) {
   swap16(r[2], r[3]);
 }
 
+// ----------------------------------------------------------------------------------- workgroup helpers
+
+constexpr int kScanThreads = 1024;                 // workgroup size of the scan below
+constexpr int kScanWaves = kScanThreads / kWave;
+
+// Inclusive prefix sum over a 1024-thread workgroup of one value per thread; wsum is kScanWaves
+// ints of LDS. Every thread of the workgroup must call it (it holds three barriers).
+__device__ __forceinline__ int block_incl_scan(int v, int* wsum) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int o = __shfl_up(v, d, kWave);
+    if (lane >= d) v += o;
+  }
+  if (lane == kWave - 1) wsum[w] = v;
+  __syncthreads();
+  if (w == 0) {
+    int s = lane < kScanWaves ? wsum[lane] : 0;
+#pragma unroll
+    for (int d = 1; d < kScanWaves; d <<= 1) {
+      const int o = __shfl_up(s, d, kWave);
+      if (lane >= d) s += o;
+    }
+    if (lane < kScanWaves) wsum[lane] = s;
+  }
+  __syncthreads();
+  const int r = v + (w ? wsum[w - 1] : 0);
+  __syncthreads();
+  return r;
+}
+
+// The lanes of a wave holding the same key as this lane (one ballot per bit of the key's
+// nbits bits, so the cost does not depend on how many distinct keys the wave holds).
+__device__ __forceinline__ uint64_t match_key(int key, int nbits) {
+  uint64_t same = ~0ull;
+  for (int b = 0; b < nbits; ++b) {
+    const bool bit = (key >> b) & 1;
+    const uint64_t bal = __ballot(bit);
+    same &= bit ? bal : ~bal;
+  }
+  return same;
+}
+
 // ----------------------------------------------------------------------------------- host side
 
 void set_error(const std::string& msg);

@@ -14,9 +14,11 @@ struct MoeArgs {
   void* out;             // GLU: act [slots, N] (activation dtype); down: y [slots, N] float
   int64_t s_om;          //   (or, with y16, y in the activation dtype)
   bh_hex_proj w0, w1;    // gate, up (GLU) or down (w0 only)
-  const int32_t* sid;
+  const int32_t* sid;     // the slot plan (align's outputs), unless ids is set
   const int32_t* eid;
   const int32_t* npp;
+  const void* ids;        // routing ids [num_slots] (I32 or I64): the kernel sorts them itself
+  int32_t ids_i64;
   const int32_t* lookup;
   const float* topk_w;
   int64_t num_slots;

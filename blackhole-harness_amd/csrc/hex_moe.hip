@@ -14,9 +14,7 @@ namespace bh {
 template <int BITS, int ADT, bool GLU, int MT, int SB, bool KF>
 __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
   __shared__ MoeSmem<BITS, GLU, MT> sm;
-  const Ranges rg = moe_ranges(a.npp[0] / (16 * MT), a.N, a.K, gridDim.x);
-  if ((int64_t)blockIdx.x >= rg.G) return;
-  moe_range<BITS, ADT, GLU, MT, SB, KF>(a, sm, blockIdx.x, rg, a.lookup, a.sid, a.eid, threadIdx.x);
+  moe_range<BITS, ADT, GLU, MT, SB, KF>(a, sm, blockIdx.x, threadIdx.x);
 }
 
 // ----------------------------------------------------------------------------------- reduction
@@ -140,10 +138,23 @@ static Workspace workspace_layout(int64_t num_blocks, int64_t n_out, int64_t n_i
   return w;
 }
 
-// Shared argument checks of the two fused entry points; fills the plan part of MoeArgs.
-static int check_moe(const char* who, int32_t bits, int32_t adt, int64_t n_out, int64_t n_in, const int32_t* sid,
-                     const int32_t* eid, int64_t num_blocks, const int32_t* npp, const int32_t* lookup,
-                     int32_t n_experts, int64_t num_slots, const bh_hex_tile* tile, int* mt, int* sb, MoeArgs& a) {
+// Where a launch's slot plan comes from: the align kernel's outputs (sid, eid, npp over
+// num_blocks blocks), or the routing ids themselves (ids), which the decode kernels sort in
+// their own workgroups.
+struct PlanSrc {
+  const int32_t* sid;
+  const int32_t* eid;
+  int64_t num_blocks;
+  const int32_t* npp;
+  const void* ids;
+  int32_t ids_dtype;
+};
+
+// Shared argument checks of the fused entry points; fills the plan part of MoeArgs. With ids the
+// plan's block count is align()'s upper bound ceil(S / block_m) + min(n_experts, S).
+static int check_moe(const char* who, int32_t bits, int32_t adt, int64_t n_out, int64_t n_in, PlanSrc& pl,
+                     const int32_t* lookup, int32_t n_experts, int64_t num_slots, const bh_hex_tile* tile, int* mt,
+                     MoeArgs& a) {
   if (bits != 3 && bits != 4) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": bits must be 3 or 4");
   if (adt != BH_HEX_BF16 && adt != BH_HEX_F16)
     return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": activations must be BF16 or F16");
@@ -153,22 +164,34 @@ static int check_moe(const char* who, int32_t bits, int32_t adt, int64_t n_out, 
   if (tile->block_n != kRows || tile->k_split != 1)
     return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": block_n must be 256 and k_split 1");
   if (n_out <= 0 || n_out > (1 << 30) || n_in > (1 << 30)) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": bad width");
-  if (n_experts <= 0 || num_slots < 0 || num_blocks < 0 || num_blocks > INT32_MAX)
-    return fail(BH_HEX_ERR_VALUE, std::string(who) + ": bad plan sizes");
+  if (n_experts <= 0 || num_slots < 0) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": bad plan sizes");
   if (n_experts > kMaxExperts)
     return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": at most 1024 experts");
-  if (num_blocks > 0 && (!sid || !eid || !npp || !lookup))
-    return fail(BH_HEX_ERR_VALUE, std::string(who) + ": null plan pointer");
+  if (pl.ids) {
+    if (tile->block_m == 128)
+      return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": block_m 128 takes a plan from the align kernel");
+    if (num_slots > kPlanMaxSlots)
+      return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": the kernels sort at most 1024 slots themselves");
+    if (pl.ids_dtype != BH_HEX_I32 && pl.ids_dtype != BH_HEX_I64)
+      return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": ids dtype must be I32 or I64");
+    if (!lookup) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": null lookup");
+    pl.num_blocks = cdiv(num_slots, tile->block_m) + std::min<int64_t>(n_experts, num_slots);
+  } else {
+    if (pl.num_blocks < 0 || pl.num_blocks > INT32_MAX) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": bad plan sizes");
+    if (pl.num_blocks > 0 && (!pl.sid || !pl.eid || !pl.npp || !lookup))
+      return fail(BH_HEX_ERR_VALUE, std::string(who) + ": null plan pointer");
+  }
   *mt = tile->block_m / 16;
-  a.sid = sid;
-  a.eid = eid;
-  a.npp = npp;
+  a.sid = pl.sid;
+  a.eid = pl.eid;
+  a.npp = pl.npp;
+  a.ids = pl.ids;
+  a.ids_i64 = pl.ids_dtype == BH_HEX_I64;
   a.lookup = lookup;
   a.n_experts = n_experts;
   a.num_slots = num_slots;
   a.N = (int32_t)n_out;
   a.K = (int32_t)n_in;
-  (void)sb;
   return BH_HEX_OK;
 }
 
@@ -181,9 +204,14 @@ static int attach_workspace(const char* who, int32_t* counters, int64_t n_counte
     return fail(BH_HEX_ERR_VALUE, std::string(who) + ": workspace smaller than bh_hex_moe_workspace() asks");
   if (!aligned(partials, 16)) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": partials must be 16-byte aligned");
   if (w.partials * 4 > (int64_t)kMaxRecords) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": plan too large");
+  // the kernels cut the units into ranges in 32-bit arithmetic: units x workgroups must fit in 31 bits
+  const int64_t g = moe_grid(num_blocks, n_out, n_in, mt);
+  const int64_t units = num_blocks * cdiv(n_out, kRows) * cdiv(cdiv(n_in, kHexBlock), 8);
+  if (units * (g + 1) >= (int64_t)1 << 31)
+    return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": plan too large for the decode kernels");
   a.counters = counters;
   a.part = partials;
-  *grid = dim3((unsigned)moe_grid(num_blocks, n_out, n_in, mt));
+  *grid = dim3((unsigned)g);
   return BH_HEX_OK;
 }
 
@@ -205,21 +233,14 @@ int proj_setup(const char* who, const bh_hex_proj* w, int bits, int64_t n_out, i
   return BH_HEX_OK;
 }
 
-}  // namespace bh
 
-using namespace bh;
-
-extern "C" int bh_hex_moe_glu(const void* x, int32_t x_dtype, int64_t s_xm, void* act, int64_t s_am,
-                              const bh_hex_proj* gate, const bh_hex_proj* up, int32_t bits, int64_t n_out, int64_t n_in,
-                              const int32_t* sorted_ids, const int32_t* expert_ids, int64_t num_blocks,
-                              const int32_t* npp, const int32_t* lookup, int32_t n_experts, int64_t num_slots,
-                              int32_t a_div, const bh_hex_tile* tile, int32_t* counters, int64_t n_counters,
-                              float* partials, int64_t n_partials, void* stream) {
-  const char* who = "bh_hex_moe_glu";
+static int moe_glu(const char* who, const void* x, int32_t x_dtype, int64_t s_xm, void* act, int64_t s_am,
+                   const bh_hex_proj* gate, const bh_hex_proj* up, int32_t bits, int64_t n_out, int64_t n_in, PlanSrc pl,
+                   const int32_t* lookup, int32_t n_experts, int64_t num_slots, int32_t a_div, const bh_hex_tile* tile,
+                   int32_t* counters, int64_t n_counters, float* partials, int64_t n_partials, void* stream) {
   MoeArgs a{};
   int mt = 0, sb = 0, words = 1;
-  int rc = check_moe(who, bits, x_dtype, n_out, n_in, sorted_ids, expert_ids, num_blocks, npp, lookup, n_experts,
-                     num_slots, tile, &mt, &sb, a);
+  int rc = check_moe(who, bits, x_dtype, n_out, n_in, pl, lookup, n_experts, num_slots, tile, &mt, a);
   if (rc) return rc;
   if ((rc = proj_setup(who, gate, bits, n_out, n_in, &sb, &words))) return rc;
   if ((rc = proj_setup(who, up, bits, n_out, n_in, &sb, &words))) return rc;
@@ -228,7 +249,7 @@ extern "C" int bh_hex_moe_glu(const void* x, int32_t x_dtype, int64_t s_xm, void
   if (s_xm % 8 || !aligned(x, 16)) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": x rows must be 16-byte aligned");
   if (cdiv(num_slots, a_div) * s_xm * 2 > (int64_t)kMaxRecords)
     return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": x over 2 GiB");
-  if (num_blocks == 0 || num_slots == 0) return BH_HEX_OK;
+  if (pl.num_blocks == 0 || num_slots == 0) return BH_HEX_OK;
   a.x = reinterpret_cast<const uint16_t*>(x);
   a.s_xm = s_xm;
   a.out = act;
@@ -237,25 +258,22 @@ extern "C" int bh_hex_moe_glu(const void* x, int32_t x_dtype, int64_t s_xm, void
   a.w1 = *up;
   a.a_div = a_div;
   a.scale_words = words;
-  if (mt == kGemmMt) return gemm_run(who, true, bits, x_dtype, sb, a, num_blocks, reinterpret_cast<hipStream_t>(stream));
+  if (mt == kGemmMt) return gemm_run(who, true, bits, x_dtype, sb, a, pl.num_blocks, reinterpret_cast<hipStream_t>(stream));
   dim3 grid;
-  if ((rc = attach_workspace(who, counters, n_counters, partials, n_partials, num_blocks, n_out, n_in, mt, true, a,
+  if ((rc = attach_workspace(who, counters, n_counters, partials, n_partials, pl.num_blocks, n_out, n_in, mt, true, a,
                              &grid))) return rc;
   launch_moe<true>(bits, x_dtype, mt, sb, grid, reinterpret_cast<hipStream_t>(stream), a);
   return check_launch(who);
 }
 
-extern "C" int bh_hex_moe_down(const void* act, int32_t act_dtype, int64_t s_am, void* y, int32_t y_dtype, int64_t s_ym,
-                               const bh_hex_proj* down, int32_t bits, int64_t n_out, int64_t n_in,
-                               const int32_t* sorted_ids, const int32_t* expert_ids, int64_t num_blocks,
-                               const int32_t* npp, const int32_t* lookup, int32_t n_experts, int64_t num_slots,
-                               const float* topk_w, const bh_hex_tile* tile, int32_t* counters, int64_t n_counters,
-                               float* partials, int64_t n_partials, void* stream) {
-  const char* who = "bh_hex_moe_down";
+static int moe_down(const char* who, const void* act, int32_t act_dtype, int64_t s_am, void* y, int32_t y_dtype,
+                    int64_t s_ym, const bh_hex_proj* down, int32_t bits, int64_t n_out, int64_t n_in, PlanSrc pl,
+                    const int32_t* lookup, int32_t n_experts, int64_t num_slots, const float* topk_w,
+                    const bh_hex_tile* tile, int32_t* counters, int64_t n_counters, float* partials, int64_t n_partials,
+                    void* stream) {
   MoeArgs a{};
   int mt = 0, sb = 0, words = 1;
-  int rc = check_moe(who, bits, act_dtype, n_out, n_in, sorted_ids, expert_ids, num_blocks, npp, lookup, n_experts,
-                     num_slots, tile, &mt, &sb, a);
+  int rc = check_moe(who, bits, act_dtype, n_out, n_in, pl, lookup, n_experts, num_slots, tile, &mt, a);
   if (rc) return rc;
   if ((rc = proj_setup(who, down, bits, n_out, n_in, &sb, &words))) return rc;
   if (!act || !y || !topk_w) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": null pointer");
@@ -264,7 +282,7 @@ extern "C" int bh_hex_moe_down(const void* act, int32_t act_dtype, int64_t s_am,
   if (s_am % 8 || !aligned(act, 16)) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": act rows must be 16-byte aligned");
   if (num_slots * s_am * 2 > (int64_t)kMaxRecords)
     return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": act over 2 GiB");
-  if (num_blocks == 0 || num_slots == 0) return BH_HEX_OK;
+  if (pl.num_blocks == 0 || num_slots == 0) return BH_HEX_OK;
   a.x = reinterpret_cast<const uint16_t*>(act);
   a.s_xm = s_am;
   a.out = y;
@@ -275,12 +293,61 @@ extern "C" int bh_hex_moe_down(const void* act, int32_t act_dtype, int64_t s_am,
   a.topk_w = topk_w;
   a.a_div = 1;
   a.scale_words = words;
-  if (mt == kGemmMt) return gemm_run(who, false, bits, act_dtype, sb, a, num_blocks, reinterpret_cast<hipStream_t>(stream));
+  if (mt == kGemmMt) return gemm_run(who, false, bits, act_dtype, sb, a, pl.num_blocks, reinterpret_cast<hipStream_t>(stream));
   dim3 grid;
-  if ((rc = attach_workspace(who, counters, n_counters, partials, n_partials, num_blocks, n_out, n_in, mt, false, a,
+  if ((rc = attach_workspace(who, counters, n_counters, partials, n_partials, pl.num_blocks, n_out, n_in, mt, false, a,
                              &grid))) return rc;
   launch_moe<false>(bits, act_dtype, mt, sb, grid, reinterpret_cast<hipStream_t>(stream), a);
   return check_launch(who);
+}
+
+}  // namespace bh
+
+using namespace bh;
+
+extern "C" int bh_hex_moe_glu(const void* x, int32_t x_dtype, int64_t s_xm, void* act, int64_t s_am,
+                              const bh_hex_proj* gate, const bh_hex_proj* up, int32_t bits, int64_t n_out, int64_t n_in,
+                              const int32_t* sorted_ids, const int32_t* expert_ids, int64_t num_blocks,
+                              const int32_t* npp, const int32_t* lookup, int32_t n_experts, int64_t num_slots,
+                              int32_t a_div, const bh_hex_tile* tile, int32_t* counters, int64_t n_counters,
+                              float* partials, int64_t n_partials, void* stream) {
+  return moe_glu("bh_hex_moe_glu", x, x_dtype, s_xm, act, s_am, gate, up, bits, n_out, n_in,
+                 PlanSrc{sorted_ids, expert_ids, num_blocks, npp, nullptr, 0}, lookup, n_experts, num_slots, a_div, tile,
+                 counters, n_counters, partials, n_partials, stream);
+}
+
+extern "C" int bh_hex_moe_glu_ids(const void* x, int32_t x_dtype, int64_t s_xm, void* act, int64_t s_am,
+                                  const bh_hex_proj* gate, const bh_hex_proj* up, int32_t bits, int64_t n_out,
+                                  int64_t n_in, const void* topk_ids, int32_t ids_dtype, const int32_t* lookup,
+                                  int32_t n_experts, int64_t num_slots, int32_t a_div, const bh_hex_tile* tile,
+                                  int32_t* counters, int64_t n_counters, float* partials, int64_t n_partials,
+                                  void* stream) {
+  if (!topk_ids && num_slots > 0) return fail(BH_HEX_ERR_VALUE, "bh_hex_moe_glu_ids: null ids");
+  return moe_glu("bh_hex_moe_glu_ids", x, x_dtype, s_xm, act, s_am, gate, up, bits, n_out, n_in,
+                 PlanSrc{nullptr, nullptr, 0, nullptr, topk_ids ? topk_ids : x, ids_dtype}, lookup, n_experts,
+                 num_slots, a_div, tile, counters, n_counters, partials, n_partials, stream);
+}
+
+extern "C" int bh_hex_moe_down(const void* act, int32_t act_dtype, int64_t s_am, void* y, int32_t y_dtype, int64_t s_ym,
+                               const bh_hex_proj* down, int32_t bits, int64_t n_out, int64_t n_in,
+                               const int32_t* sorted_ids, const int32_t* expert_ids, int64_t num_blocks,
+                               const int32_t* npp, const int32_t* lookup, int32_t n_experts, int64_t num_slots,
+                               const float* topk_w, const bh_hex_tile* tile, int32_t* counters, int64_t n_counters,
+                               float* partials, int64_t n_partials, void* stream) {
+  return moe_down("bh_hex_moe_down", act, act_dtype, s_am, y, y_dtype, s_ym, down, bits, n_out, n_in,
+                  PlanSrc{sorted_ids, expert_ids, num_blocks, npp, nullptr, 0}, lookup, n_experts, num_slots, topk_w,
+                  tile, counters, n_counters, partials, n_partials, stream);
+}
+
+extern "C" int bh_hex_moe_down_ids(const void* act, int32_t act_dtype, int64_t s_am, void* y, int32_t y_dtype,
+                                   int64_t s_ym, const bh_hex_proj* down, int32_t bits, int64_t n_out, int64_t n_in,
+                                   const void* topk_ids, int32_t ids_dtype, const int32_t* lookup, int32_t n_experts,
+                                   int64_t num_slots, const float* topk_w, const bh_hex_tile* tile, int32_t* counters,
+                                   int64_t n_counters, float* partials, int64_t n_partials, void* stream) {
+  if (!topk_ids && num_slots > 0) return fail(BH_HEX_ERR_VALUE, "bh_hex_moe_down_ids: null ids");
+  return moe_down("bh_hex_moe_down_ids", act, act_dtype, s_am, y, y_dtype, s_ym, down, bits, n_out, n_in,
+                  PlanSrc{nullptr, nullptr, 0, nullptr, topk_ids ? topk_ids : act, ids_dtype}, lookup, n_experts,
+                  num_slots, topk_w, tile, counters, n_counters, partials, n_partials, stream);
 }
 
 extern "C" int bh_hex_moe_workspace(int64_t num_blocks, int64_t n_out, int64_t n_in, int32_t block_m, int32_t glu,

@@ -86,27 +86,47 @@ template <int MT, int NM>
 constexpr int part_floats() { return MT * NM * kWave * 4; }
 
 // Range g of G holding unit u of U.
-__device__ __forceinline__ int owner(int64_t u, int64_t U, int64_t G) {
+// (32-bit arithmetic throughout: the host refuses launches whose U * G does not fit in 31 bits,
+// and 64-bit divisions would cost hundreds of scalar instructions each before the first load.)
+__device__ __forceinline__ int owner(uint32_t u, uint32_t U, uint32_t G) {
   return (int)(((u + 1) * G + U - 1) / U - 1);
 }
 
 // The cut of a launch's units into ranges, for `used` plan blocks over an N x K projection
-// and `grid` workgroups. With between half and all as many items as workgroups, each range is
-// one whole item: no item is split, so no partial sums are exchanged. Otherwise the units are
-// spread evenly over min(grid, U) ranges, splitting items.
+// and `grid` workgroups. Whole items when that balances well enough: with q = ceil(items / grid)
+// items per range, q = 1 and at least half as many items as workgroups, or q > 1 and the ranges
+// at least 3/4 full on average; then Q = q and range g is items [g q, (g + 1) q), so no item is
+// split and no partial sums are exchanged. Otherwise (Q = 0) the units are spread evenly over
+// min(grid, U) ranges, splitting items.
 struct Ranges {
-  int64_t U, G;
+  uint32_t U, G, Q;
 };
-__host__ __device__ __forceinline__ Ranges moe_ranges(int64_t used, int N, int K, int64_t grid) {
-  const int64_t nrt = (N + kRows - 1) / kRows;
-  const int64_t nun = (K / kHexBlock + 7) / 8;
-  const int64_t items = used * nrt;
+__host__ __device__ __forceinline__ Ranges moe_ranges(uint32_t used, int N, int K, uint32_t grid) {
+  const uint32_t nrt = (uint32_t)(N + kRows - 1) / kRows;
+  const uint32_t nun = ((uint32_t)K / kHexBlock + 7) / 8;
+  const uint32_t items = used * nrt;
   Ranges r;
   r.U = items * nun;
-  const bool whole = items <= grid && 2 * items >= grid;
-  r.G = whole ? items : (grid < r.U ? grid : r.U);
+  const uint32_t q = (items + grid - 1) / grid;
+  const bool whole = items > 0 && (q == 1 ? 2 * items >= grid : 4 * items >= 3 * q * grid);
+  r.Q = whole ? q : 0;
+  r.G = whole ? (items + q - 1) / q : (grid < r.U ? grid : r.U);
   return r;
 }
+
+// The most slots a launch may sort in its own workgroups (one per thread) instead of taking a
+// plan from the align kernel.
+constexpr int kPlanMaxSlots = kThreads;
+
+// LDS of the in-kernel slot plan (it lives where the activation ring will, before the ring's
+// first use): slots of each (wave, expert), as bytes (a wave holds at most 64 slots), the
+// expert's first block, and the scan's wave sums.
+struct PlanLds {
+  uint8_t wcnt[kWaves][kMaxExperts];
+  int first[kMaxExperts];
+  int wsum[kWaves];
+  int used;
+};
 
 // LDS of one range. The pair tables come first: their base stays inside the ds offset field.
 template <int BITS, bool GLU, int MT>
@@ -114,7 +134,10 @@ struct alignas(16) MoeSmem {
   static constexpr int L = 1 << BITS, NPAIR = 1 << (2 * BITS), NM = GLU ? 2 : 1, BM = 16 * MT;
   static constexpr int P = trip<MT, GLU>(), MAXBLK = kMaxBlk16 / MT, TILE = MT * 1024;
   uint32_t tab[NPAIR * 64];
-  uint32_t ring[2][P * 2 * TILE];        // a trip's activation tiles, two trips
+  union {
+    uint32_t ring[2][P * 2 * TILE];      // a trip's activation tiles, two trips
+    PlanLds plan;                        // the in-kernel slot plan (prologue only)
+  };
   int lut[kMaxExperts];                  // the tier lookup
   int slots[MAXBLK * BM];                // slot rows of the range's blocks
   float slot_w[GLU ? 1 : MAXBLK * BM];   // their top-k weights (down)
@@ -126,9 +149,8 @@ struct alignas(16) MoeSmem {
 };
 
 template <int BITS, int ADT, bool GLU, int MT, int SB, bool KF>
-__device__ __forceinline__ void moe_range(const MoeArgs& a, MoeSmem<BITS, GLU, MT>& sm, int64_t g, const Ranges& rg,
-                                          const int* lut_src, const int32_t* plan_sid, const int32_t* plan_eid,
-                                          const int tid) {
+__device__ __forceinline__ void moe_range(const MoeArgs& a, MoeSmem<BITS, GLU, MT>& sm, const uint32_t g, const int tid) {
+  static_assert(sizeof(PlanLds) <= sizeof(sm.ring), "the plan's LDS must fit in the ring");
   constexpr int L = 1 << BITS;
   constexpr int NPAIR = 1 << (2 * BITS);
   constexpr int NM = GLU ? 2 : 1;
@@ -157,19 +179,77 @@ __device__ __forceinline__ void moe_range(const MoeArgs& a, MoeSmem<BITS, GLU, M
   const int nb32 = a.K / kHexBlock;
   const int nun = (nb32 + 7) / 8;                              // units per item
 
+  // ---- the slot plan from the routing ids (a.ids set): every workgroup sorts the slots by
+  // expert in LDS, with the align kernel's algorithm and result (a stable counting sort, each
+  // expert's run padded to whole blocks), and keeps the part its range needs. A thread per
+  // slot: a wave finds the lanes holding its key by ballots; the key's lowest lane records the
+  // wave's count; one pass over the waves gives each expert's total, a workgroup scan its first
+  // block, and each slot's row is that block's first row + the expert's slots in earlier waves
+  // + its rank among the wave's lanes of the same key.
+  uint32_t used;
+  int my_row = -1, my_nb = 0, my_first = 0;     // this thread's slot row; its expert's blocks
+  if (a.ids) {
+    PlanLds& ps = sm.plan;
+    const int S = (int)a.num_slots, E = a.n_experts;
+    const int nw = (S + kWave - 1) / kWave;
+    int64_t id = -1;
+    if (tid < S) id = a.ids_i64 ? reinterpret_cast<const int64_t*>(a.ids)[tid] : reinterpret_cast<const int32_t*>(a.ids)[tid];
+    if (tid < E) lut[tid] = a.lookup[tid];
+    for (int i = tid; i < nw * (kMaxExperts / 4); i += kThreads) reinterpret_cast<uint32_t*>(ps.wcnt)[i] = 0u;
+    __syncthreads();
+    const int key = (id >= 0 && id < E && lut[id] >= 0) ? (int)id : E;
+    int nbits = 1;
+    while ((1 << nbits) <= E) ++nbits;        // keys in [0, E] (E: not placed)
+    const uint64_t same = match_key(key, nbits);
+    const int rank = __popcll(same & (lane ? (~0ull >> (64 - lane)) : 0ull));
+    if (key < E && rank == 0) ps.wcnt[wave][key] = (uint8_t)__popcll(same);
+    __syncthreads();
+    int c = 0, before = 0;
+    if (tid < E)
+      for (int v = 0; v < nw; ++v) c += ps.wcnt[v][tid];
+    if (key < E)
+      for (int v = 0; v < wave; ++v) before += ps.wcnt[v][key];
+    my_nb = (c + BM - 1) / BM;
+    const int incl = block_incl_scan(my_nb, ps.wsum);   // (its barriers order the reads above)
+    my_first = incl - my_nb;
+    if (tid < E) ps.first[tid] = my_first;
+    if (tid == kThreads - 1) ps.used = incl;
+    __syncthreads();
+    used = ps.used;
+    if (key < E) my_row = ps.first[key] * BM + before + rank;
+  } else {
+    used = a.npp[0] / BM;
+  }
+  const Ranges rg = moe_ranges(used, a.N, a.K, gridDim.x);
+  if (g >= rg.G) return;                                       // (uniform: no work for this workgroup)
+
   // ---- this range of units over the used blocks
-  const int64_t U = rg.U, G = rg.G;
-  const int64_t ub = U * g / G, ue = U * (g + 1) / G;
+  const uint32_t U = rg.U, G = rg.G;
+  const uint32_t ub = rg.Q ? g * rg.Q * nun : U * g / G;
+  const uint32_t ue = rg.Q ? min(U, (g + 1) * rg.Q * nun) : U * (g + 1) / G;
   const int n = (int)(ue - ub);
-  const int64_t item0 = ub / nun, item1 = (ue - 1) / nun;
-  const int64_t pm0 = item0 / nrt;
+  const uint32_t item0 = ub / nun, item1 = (ue - 1) / nun;
+  const uint32_t pm0 = item0 / nrt;
   const int nblk = min((int)(item1 / nrt - pm0 + 1), MAXBLK);
 
-  // ---- stage the plan: tier lookup, block experts, slot rows
-  for (int i = tid; i < a.n_experts; i += kThreads) lut[i] = lut_src[i];
-  for (int b = tid; b < MAXBLK; b += kThreads) blk_g[b] = b < nblk ? plan_eid[pm0 + b] : -1;
-  for (int r = tid; r < MAXBLK * BM; r += kThreads)
-    slots[r] = r < nblk * BM ? plan_sid[pm0 * BM + r] : (int)a.num_slots;
+  // ---- stage the plan: tier lookup, block experts, slot rows (S for padding)
+  if (a.ids) {
+    for (int b = tid; b < MAXBLK; b += kThreads) blk_g[b] = -1;
+    for (int r = tid; r < MAXBLK * BM; r += kThreads) slots[r] = (int)a.num_slots;
+    __syncthreads();
+    // thread e holds expert e's run, blocks [my_first, my_first + my_nb): those in this range
+    const int j1 = min(my_first + my_nb, (int)pm0 + nblk);
+    for (int j = max(my_first, (int)pm0); j < j1; ++j) blk_g[j - pm0] = tid;
+    if (my_row >= 0) {
+      const int r = my_row - (int)pm0 * BM;
+      if (r >= 0 && r < nblk * BM) slots[r] = tid;
+    }
+  } else {
+    for (int i = tid; i < a.n_experts; i += kThreads) lut[i] = a.lookup[i];
+    for (int b = tid; b < MAXBLK; b += kThreads) blk_g[b] = b < nblk ? a.eid[pm0 + b] : -1;
+    for (int r = tid; r < MAXBLK * BM; r += kThreads)
+      slots[r] = r < nblk * BM ? a.sid[pm0 * BM + r] : (int)a.num_slots;
+  }
   __syncthreads();
   auto expert_of = [&](int b) {      // tier-local expert of block b, -1 for none
     const int eg = blk_g[b];
@@ -249,7 +329,7 @@ __device__ __forceinline__ void moe_range(const MoeArgs& a, MoeSmem<BITS, GLU, M
   };
 
   // ---- activation stream: the tiles of the next trip, one dword per lane per (unit, step, subtile)
-  const int x_rows = (int)((a.num_slots + a.a_div - 1) / a.a_div);
+  const int x_rows = (int)(((uint32_t)a.num_slots + (uint32_t)a.a_div - 1) / (uint32_t)a.a_div);
   const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(a.x, (int64_t)x_rows * a.s_xm * 2);
   // lane dword of a step's tile: wave w, lane l -> slot l / 4 of the subtile, inputs
   // 32 (w / 4) + 8 (w % 4) + 2 (l % 4) of the step (the fragment layout the MFMA reads)
@@ -379,8 +459,8 @@ __device__ __forceinline__ void moe_range(const MoeArgs& a, MoeSmem<BITS, GLU, M
   // A range holds at most two split items, its first and its last: their partial tiles are
   // stored (device-coherent) when the item's part ends, and the arrival counts and sums wait
   // for the end of the range, where they hold up no streaming.
-  const int64_t npart_floats = G * 2 * kWaves * PF;
-  auto part_off = [&](int64_t gg, int which, int mt, int m) {   // byte offset of this lane's float4
+  const uint32_t npart_floats = G * 2 * kWaves * PF;
+  auto part_off = [&](uint32_t gg, int which, int mt, int m) {   // byte offset of this lane's float4
     return (int)((((gg * 2 + which) * kWaves + wave) * PF + (mt * NM + m) * kWave * 4 + lane * 4) * 4);
   };
   auto real_rows = [&](int b, int mt) {    // does this lane hold any real slot row?
@@ -446,7 +526,7 @@ __device__ __forceinline__ void moe_range(const MoeArgs& a, MoeSmem<BITS, GLU, M
     if (n_split == 0) return;            // (uniform: all waves share the range)
     __builtin_amdgcn_s_waitcnt(0);       // this wave's partial tiles are visible device-wide
     __syncthreads();                     // ... and every wave's
-    int64_t it[2];
+    uint32_t it[2];
     int g_lo[2], g_hi[2];
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
@@ -492,22 +572,11 @@ __device__ __forceinline__ void moe_range(const MoeArgs& a, MoeSmem<BITS, GLU, M
     }
   };
 
-  // ---- prologue: the rest of the staging (its waits leave nothing in flight), then the
-  // pipeline's first loads in the loop's order: activation tiles, weights, and the first trip's
-  // tiles published.
-  for (int b = tid; b < MAXBLK; b += kThreads) {
-    const int e = expert_of(b);
-    blk_e[b] = e;
-#pragma unroll
-    for (int m = 0; m < NM; ++m) blk_es[b][m] = e >= 0 ? (m == 0 ? a.w0 : a.w1).expert_scale[e] : 0.f;
-  }
-  if constexpr (!GLU)
-    for (int r = tid; r < MAXBLK * BM; r += kThreads) slot_w[r] = slots[r] < a.num_slots ? a.topk_w[slots[r]] : 0.f;
-  for (int i = tid; i < MAXBLK * NM * L; i += kThreads) {
-    const int b = i / (NM * L), m = (i / L) % NM, c = i % L;
-    const int e = expert_of(b);
-    blk_lv[b][m][c] = e >= 0 ? (uint16_t)to_bits<ADT>((m == 0 ? a.w0 : a.w1).levels[(int64_t)e * L + c]) : 0;
-  }
+  // ---- prologue. The rest of the staging (expert scales, top-k weights, levels) is loaded into
+  // registers first, then the first trip's activation tiles and weights are requested; the
+  // staged values are then stored (their wait leaves the trip's loads in flight) and the first
+  // block's pair tables built while those loads arrive. Then the first trip's tiles are
+  // published and the second trip's requested.
   Pos cp{0, (int)(item0 - pm0 * nrt), (int)(ub - item0 * nun)};
   Pos lp = cp;
   Stage<BITS, NM, SB, KF> st[P];
@@ -530,21 +599,60 @@ __device__ __forceinline__ void moe_range(const MoeArgs& a, MoeSmem<BITS, GLU, M
       ++jl;
     }
   };
+  constexpr int NLV = (MAXBLK * NM * L + kThreads - 1) / kThreads;   // staged values per thread
+  constexpr int NSW = (MAXBLK * BM + kThreads - 1) / kThreads;
+  static_assert(MAXBLK <= kThreads, "one thread per block's expert scales");
+  const int e_own = tid < MAXBLK ? expert_of(tid) : -1;
+  float es_v[NM], lv_v[NLV], sw_v[NSW];
+#pragma unroll
+  for (int m = 0; m < NM; ++m) es_v[m] = e_own >= 0 ? (m == 0 ? a.w0 : a.w1).expert_scale[e_own] : 0.f;
+#pragma unroll
+  for (int q = 0; q < NLV; ++q) {
+    const int i = q * kThreads + tid;
+    const int b = i / (NM * L), m = (i / L) % NM, c = i % L;
+    const int e = i < MAXBLK * NM * L ? expert_of(b) : -1;
+    lv_v[q] = e >= 0 ? (m == 0 ? a.w0 : a.w1).levels[(int64_t)e * L + c] : 0.f;
+  }
+#pragma unroll
+  for (int q = 0; q < NSW; ++q) {
+    const int r = q * kThreads + tid;
+    sw_v[q] = (!GLU && r < MAXBLK * BM && slots[r] < a.num_slots) ? a.topk_w[slots[r]] : 0.f;
+  }
   __builtin_amdgcn_sched_barrier(0);
   act_trip();
   __builtin_amdgcn_sched_barrier(0);
   first_weights();
   __builtin_amdgcn_sched_barrier(0);
-  publish(ring[0]);
+  if (tid < MAXBLK) {
+    blk_e[tid] = e_own;
+#pragma unroll
+    for (int m = 0; m < NM; ++m) blk_es[tid][m] = es_v[m];
+  }
+#pragma unroll
+  for (int q = 0; q < NLV; ++q) {
+    const int i = q * kThreads + tid;
+    if (i < MAXBLK * NM * L) (&blk_lv[0][0][0])[i] = (uint16_t)to_bits<ADT>(lv_v[q]);
+  }
+  if constexpr (!GLU)
+#pragma unroll
+    for (int q = 0; q < NSW; ++q) {
+      const int r = q * kThreads + tid;
+      if (r < MAXBLK * BM) slot_w[r] = sw_v[q];
+    }
+  __syncthreads();                     // the staged plan is complete
+  const int e_first = __builtin_amdgcn_readfirstlane(blk_e[0]);   // (a range starts at its block 0)
+  if (e_first >= 0) build_table(0);
+  __builtin_amdgcn_sched_barrier(0);
+  publish(ring[0]);                    // (the plan's LDS under the ring is no longer read)
   __builtin_amdgcn_sched_barrier(0);
   act_trip();
   __builtin_amdgcn_sched_barrier(0);
-  __syncthreads();                     // the first trip's tiles and the staged plan are complete
+  __syncthreads();                     // the first trip's tiles and the first tables are complete
 
   // ---- main loop: one trip of P units per iteration. Loads per trip, in order: per unit the
   // weights of the unit P ahead, then the activation tiles of the trip after next. The next
   // trip's tiles go into the other ring stage at the end, under one barrier per trip.
-  int cur_e = -1, cur_b = -1, e = -1, sa = 0;
+  int cur_b = 0, cur_e = e_first, e = e_first, sa = 0;     // block 0's tables are built
   bool first = true;
   for (int j0 = 0; j0 < n; j0 += P) {
     const int t = j0 / P;

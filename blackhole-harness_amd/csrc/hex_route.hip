@@ -123,42 +123,6 @@ __device__ __forceinline__ int64_t placed_id(const void* p, int64_t i, int32_t n
   else return (e >= 0 && e < n) ? e : -1;
 }
 
-// Inclusive prefix sum over the workgroup of one value per thread (1024 threads).
-__device__ int block_incl_scan(int v, int* wsum) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const int o = __shfl_up(v, d, kWave);
-    if (lane >= d) v += o;
-  }
-  if (lane == kWave - 1) wsum[w] = v;
-  __syncthreads();
-  if (w == 0) {
-    int s = lane < kAlignWaves ? wsum[lane] : 0;
-#pragma unroll
-    for (int d = 1; d < kAlignWaves; d <<= 1) {
-      const int o = __shfl_up(s, d, kWave);
-      if (lane >= d) s += o;
-    }
-    if (lane < kAlignWaves) wsum[lane] = s;
-  }
-  __syncthreads();
-  const int r = v + (w ? wsum[w - 1] : 0);
-  __syncthreads();
-  return r;
-}
-
-// The lanes of a wave holding the same key as this lane (ballots over the key's nbits bits).
-__device__ __forceinline__ uint64_t match_key(int key, int nbits) {
-  uint64_t same = ~0ull;
-  for (int b = 0; b < nbits; ++b) {
-    const bool bit = (key >> b) & 1;
-    const uint64_t bal = __ballot(bit);
-    same &= bit ? bal : ~bal;
-  }
-  return same;
-}
-
 // Stable counting sort of the slots by expert, each expert's run padded to bm. Wave w owns the
 // contiguous slot range [w P, (w + 1) P): it counts its slots per expert (lanes with the same
 // key found by ballots over the key bits, so each key is counted once per 64-slot chunk), one

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define BH_HEX_ABI_VERSION 7
+#define BH_HEX_ABI_VERSION 8
 
 enum bh_hex_status {
   BH_HEX_OK = 0,
@@ -161,6 +161,29 @@ int bh_hex_moe_down(const void* act, int32_t act_dtype, int64_t s_am, void* y, i
                     const int32_t* lookup, int32_t n_experts, int64_t num_slots, const float* topk_w,
                     const bh_hex_tile* tile, int32_t* counters, int64_t n_counters, float* partials,
                    int64_t n_partials, void* stream);
+
+/* bh_hex_moe_glu without a precomputed plan: the kernel derives the slot plan from the routing
+ * ids itself (topk_ids [num_slots], I32 or I64), as align() with this tier's lookup would
+ * (hex_moe.py:201-222): every workgroup sorts the slots by expert in LDS and keeps the blocks
+ * its range needs, so no align launch precedes it. block_m 16, 32 or 64 (the decode kernels)
+ * and at most 1024 slots; otherwise BH_HEX_ERR_UNSUPPORTED. The workspace is
+ * bh_hex_moe_workspace(bh_hex_align_max_blocks(num_slots, n_experts, block_m), ...). Same
+ * results as align + bh_hex_moe_glu. Replaces align and the first _hex_moe_kernel launch of
+ * hex_moe_fused (hex_moe.py:201-222, 318-322). */
+int bh_hex_moe_glu_ids(const void* x, int32_t x_dtype, int64_t s_xm, void* act, int64_t s_am,
+                       const bh_hex_proj* gate, const bh_hex_proj* up, int32_t bits, int64_t n_out, int64_t n_in,
+                       const void* topk_ids, int32_t ids_dtype, const int32_t* lookup, int32_t n_experts,
+                       int64_t num_slots, int32_t a_div, const bh_hex_tile* tile, int32_t* counters,
+                       int64_t n_counters, float* partials, int64_t n_partials, void* stream);
+
+/* bh_hex_moe_down with the plan derived from the routing ids in the kernel, as
+ * bh_hex_moe_glu_ids (same limits and workspace). Replaces the second _hex_moe_kernel launch of
+ * hex_moe_fused (hex_moe.py:324) together with the plan it reads. */
+int bh_hex_moe_down_ids(const void* act, int32_t act_dtype, int64_t s_am, void* y, int32_t y_dtype, int64_t s_ym,
+                        const bh_hex_proj* down, int32_t bits, int64_t n_out, int64_t n_in, const void* topk_ids,
+                        int32_t ids_dtype, const int32_t* lookup, int32_t n_experts, int64_t num_slots,
+                        const float* topk_w, const bh_hex_tile* tile, int32_t* counters, int64_t n_counters,
+                        float* partials, int64_t n_partials, void* stream);
 
 /* Device workspace that bh_hex_moe_glu (glu != 0) or bh_hex_moe_down needs for a plan of
  * num_blocks blocks of block_m slots over n_out x n_in projections on the current device:

@@ -45,13 +45,23 @@ def rel_err(got: torch.Tensor, want: torch.Tensor) -> float:
 
 
 # (name, E, H, I, k, tiers as (experts, bits), T, zipf) at 128-input scale blocks, as BASELINE
-# states them: config 3's prefill (3-bit, the 128-slot kernels), config 4's two REAQ tiers under
-# Zipf routing, config 5 at a decode and a prefill batch.
+# states them, at every batch the benchmark reports: config 2's decode sweep (16-slot blocks, the
+# kernels sorting the slots themselves), config 3's prefill (3-bit, the 128-slot kernels),
+# config 4's two REAQ tiers under Zipf routing, config 5's sweep (T=256: 32-slot blocks behind
+# the align kernel; T=8192: 65,536 slots through the chunked align and the prefill kernels).
 SHAPES = [
+    ("config2-T1", 96, 2048, 768, 8, ((96, 4),), 1, 0.0),
+    ("config2-T4", 96, 2048, 768, 8, ((96, 4),), 4, 0.0),
+    ("config2-T16", 96, 2048, 768, 8, ((96, 4),), 16, 0.0),
+    ("config2-T64", 96, 2048, 768, 8, ((96, 4),), 64, 0.0),
     ("config3", 96, 2048, 768, 8, ((96, 3),), 4096, 0.0),
     ("config4", 96, 2048, 768, 8, ((48, 4), (48, 3)), 256, 1.1),
+    ("config5-T1", 128, 4096, 1536, 8, ((128, 4),), 1, 0.0),
+    ("config5-T4", 128, 4096, 1536, 8, ((128, 4),), 4, 0.0),
     ("config5-decode", 128, 4096, 1536, 8, ((128, 4),), 16, 0.0),
+    ("config5-T256", 128, 4096, 1536, 8, ((128, 4),), 256, 0.0),
     ("config5-prefill", 128, 4096, 1536, 8, ((128, 4),), 2048, 0.0),
+    ("config5-T8192", 128, 4096, 1536, 8, ((128, 4),), 8192, 0.0),
 ]
 
 
@@ -89,3 +99,12 @@ def test_full_shape_layer(name, E, H, I, k, groups, T, zipf):
         # path="auto" keeps to the fused kernels at every batch unless BLACKHOLE_HEX_DEQUANT_MIN
         # is set (the fused results do not depend on timing, so they are equal bit for bit)
         assert torch.equal(hm.hex_moe(x, w, ids, tiers), fused)
+    if T * k <= hm.KERNEL_PLAN_MAX:
+        # the kernels' own slot plan equals the align kernel's (align_mode "vllm" maps to the align
+        # kernel at every batch), so the outputs are equal bit for bit
+        assert torch.equal(hm.hex_moe_fused(x, w, ids, tiers, align_mode="vllm"), fused)
+    if T * k <= hm.DIRECT_MAX:
+        # the reference's direct plan (one block per slot) at full width
+        err = rel_err(hm.hex_moe_fused(x, w, ids, tiers, align_mode="direct"), want)
+        say(f"  direct plan: {err:.2e}")
+        assert err < TOL_16, err

@@ -109,7 +109,8 @@ def test_dequant_all_places_experts():
                                              (2048, 96, 32, True, torch.int64), (3000, 1000, 16, False, torch.int64),
                                              (32768, 96, 64, False, torch.int64), (40000, 128, 16, True, torch.int32),
                                              (4096, 96, 128, False, torch.int64), (4097, 96, 128, True, torch.int64),
-                                             (33000, 96, 128, True, torch.int32), (20000, 1000, 128, True, torch.int64)])
+                                             (33000, 96, 128, True, torch.int32), (20000, 1000, 128, True, torch.int64),
+                                             (65536, 128, 128, False, torch.int64)])
 def test_align_bit_exact(S, n, bm, skew, idt):
     say(f"align S={S} n={n} bm={bm} skew={skew} {idt}")
     rng = np.random.default_rng(S + n + bm)
@@ -448,6 +449,62 @@ def test_three_tiers_on_three_streams():
             assert torch.equal(out, eager), (T, i)
             _ = hm.hex_moe_fused(x * 2, wd, idd, tiers, cfg)
             torch.cuda.synchronize()
+
+
+# --------------------------------------------------------------------------- the kernels' own plan
+
+
+@pytest.mark.parametrize("bm", [16, 32, 64])
+def test_kernel_plan_equals_align_plan(bm):
+    """The decode kernels sorting the slots themselves (bh_hex_moe_*_ids) give the outputs of the
+    align kernel's plan bit for bit (the same blocks, so the same unit ranges), and match the
+    oracle: one tier and two tiers, int32 and int64 ids, ids outside [0, E) and slots of experts
+    no tier holds, from 1 slot to the 1024-slot limit with up to 1000 experts."""
+    say(f"kernel plan bm={bm}")
+    cases = [(40, 256, 256, 4, 13, 1, False), (40, 256, 256, 4, 13, 5, True), (40, 256, 256, 4, 0, 33, False),
+             (40, 256, 256, 4, 0, 256, True), (1000, 256, 256, 8, 0, 128, False), (16, 512, 256, 2, 5, 7, True)]
+    for E, H, I, k, split, T, skew in cases:
+        ref, tiers = make_layer(E, H, I, split, (4, 3), seed=70 + T, block=128)
+        w, ids = routing(T, E, k, seed=T, skew=skew)
+        ids = ids.copy()
+        ids[0, 0] = -1
+        if T > 1:
+            ids[-1, -1] = E + 3
+        if E == 16:                      # a tier that does not hold every expert
+            ref, tiers = ref[:1], tiers[:1]
+        x = torch.randn(T, H, generator=torch.Generator().manual_seed(T)).to(torch.bfloat16).to(DEV)
+        wd = torch.from_numpy(w).to(DEV)
+        cfg = {"BLOCK_M": bm}
+        want = O.moe_reference(x.float().cpu().numpy(), w, ids, ref, "bf16")
+        for idt in (torch.int64, torch.int32):
+            idd = torch.from_numpy(ids).to(idt).to(DEV)
+            assert hm.KERNEL_PLAN_MAX >= T * k
+            own = hm.hex_moe_fused(x, wd, idd, tiers, cfg)
+            # align_mode "vllm" takes the align kernel at every batch (auto would take the direct
+            # plan up to 32 slots, whose different blocks split items differently)
+            aligned = hm.hex_moe_fused(x, wd, idd, tiers, cfg, align_mode="vllm")
+            assert torch.equal(own, aligned), (E, T, idt)
+            assert O.rel_err(own.float().cpu().numpy(), want) < TOL_16, (E, T, idt)
+
+
+def test_kernel_plan_limits():
+    """More than 1024 slots, or block_m 128, are refused by the _ids entry points (the Python
+    layer then launches the align kernel); 1024 slots are taken."""
+    say("kernel plan limits")
+    E, H, I, k = 8, 256, 128, 8
+    ref, tiers = make_layer(E, H, I, 0, (4,), seed=71, block=128)
+    t = tiers[0]
+    x = torch.zeros(129, H, dtype=torch.bfloat16, device=DEV)
+    act = torch.empty(129 * k, I, dtype=torch.bfloat16, device=DEV)
+    ids = torch.zeros(129 * k, dtype=torch.long, device=DEV)
+    code = 4
+    with pytest.raises(NotImplementedError, match="1024 slots"):
+        hm._launch_glu_ids(x, act, t, ids, code, 129 * k, k, 16)
+    with pytest.raises(NotImplementedError, match="block_m 128"):
+        hm._launch_glu_ids(x, act, t, ids[:1024], code, 1024, k, 128)
+    hm._launch_glu_ids(x[:128], act[:1024], t, ids[:1024], code, 1024, k, 16)
+    torch.cuda.synchronize()
+    assert run_fused(ref, tiers, 128, E, k, H, seed=3) < TOL_16       # 1024 slots through the kernels' plan
 
 
 # --------------------------------------------------------------------------- workspaces
