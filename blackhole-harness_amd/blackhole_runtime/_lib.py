@@ -61,6 +61,8 @@ SIGNATURES = {
                                        _I64, _P, _TILE, _P, _I64, _P, _I64, _P]),
     "bh_hex_moe_glu_ids": (ctypes.c_int, [_P, _I32, _I64, _P, _I64, _PROJ, _PROJ, _I32, _I64, _I64, _P, _I32, _P, _I32,
                                           _I64, _I32, _TILE, _P, _I64, _P, _I64, _P]),
+    "bh_hex_moe_glu_ids_noalloc": (ctypes.c_int, [_P, _I32, _I64, _P, _I64, _PROJ, _PROJ, _I32, _I64, _I64, _P, _I32, _P,
+                                                  _I32, _I64, _I32, _TILE, _P]),
     "bh_hex_moe_down_ids": (ctypes.c_int, [_P, _I32, _I64, _P, _I32, _I64, _PROJ, _I32, _I64, _I64, _P, _I32, _P, _I32,
                                            _I64, _P, _TILE, _P, _I64, _P, _I64, _P]),
     "bh_hex_moe_workspace": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, ctypes.POINTER(ctypes.c_int64),
@@ -68,7 +70,7 @@ SIGNATURES = {
     "bh_hex_moe_reduce": (ctypes.c_int, [_P, _I32, _I64, _P, _I32, _I32, _I64, _I32, _I64, _P, _I32, _I64, _P]),
 }
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _lib = None
 

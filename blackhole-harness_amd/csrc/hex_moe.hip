@@ -5,6 +5,8 @@
 // both roles (GLU gate/up with SiLU, and down with the top-k weight) and the torch sum at
 // hex_moe.py:325. The decode-regime kernel is one persistent launch over the ranges of
 // hex_range.h, one range per workgroup; the 128-slot prefill kernels are in hex_gemm.hip.
+#include <algorithm>
+#include <mutex>
 #include <string>
 
 #include "hex_range.h"
@@ -301,6 +303,56 @@ static int moe_down(const char* who, const void* act, int32_t act_dtype, int64_t
   return check_launch(who);
 }
 
+// ----------------------------------------------------------------------------------- static scratch
+
+// The workspace of bh_hex_moe_glu_ids_noalloc: a static device array, one copy per device,
+// held until the process ends. The first kScratchCounters words are the arrival counters
+// (zero at load, zeroed again when a device is set up, and left zero by every call); the rest
+// are partial sums (no initial value). 1 MiB of counters and 16 MiB of partials: the partials of
+// a 16-slot gate/up launch on 256 workgroups (256 x 2 x 16 waves x 2 matrices x 64 lanes x 4).
+constexpr int64_t kScratchCounters = 1 << 18;
+constexpr int64_t kScratchPartials = 1 << 22;
+static __device__ __align__(256) uint32_t scratch[kScratchCounters + kScratchPartials];
+
+__global__ void zero_words_kernel(uint32_t* p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static uint32_t* g_scratch[kMaxScratchDevices];   // device address of `scratch` per device
+
+// The device address of the stream's device's scratch. Set up once per device, with that
+// device current: the symbol's address is looked up (the array's name is only a host-side
+// stand-in) and its counters are cleared by a fill kernel on `st`, ahead of the call's kernels.
+static int scratch_for(const char* who, hipStream_t st, uint32_t** out) {
+  int dev = 0;
+  if (hipStreamGetDevice(st, &dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices)
+    return fail(BH_HEX_ERR_HIP, std::string(who) + ": cannot tell the stream's device");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    int cur = 0;
+    if (hipGetDevice(&cur) != hipSuccess) return fail(BH_HEX_ERR_HIP, std::string(who) + ": hipGetDevice failed");
+    if (cur != dev && hipSetDevice(dev) != hipSuccess)
+      return fail(BH_HEX_ERR_HIP, std::string(who) + ": hipSetDevice failed");
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e == hipSuccess && p) {
+      hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)cdiv(kScratchCounters, 256)), dim3(256), 0, st,
+                         static_cast<uint32_t*>(p), kScratchCounters);
+    }
+    const hipError_t le = hipGetLastError();
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (e != hipSuccess || !p)
+      return fail(BH_HEX_ERR_HIP, std::string(who) + ": hipGetSymbolAddress(scratch): " + hipGetErrorString(e));
+    if (le != hipSuccess) return fail(BH_HEX_ERR_HIP, std::string(who) + ": clearing the scratch: " + hipGetErrorString(le));
+    g_scratch[dev] = static_cast<uint32_t*>(p);
+  }
+  *out = g_scratch[dev];
+  return BH_HEX_OK;
+}
+
 }  // namespace bh
 
 using namespace bh;
@@ -326,6 +378,35 @@ extern "C" int bh_hex_moe_glu_ids(const void* x, int32_t x_dtype, int64_t s_xm, 
   return moe_glu("bh_hex_moe_glu_ids", x, x_dtype, s_xm, act, s_am, gate, up, bits, n_out, n_in,
                  PlanSrc{nullptr, nullptr, 0, nullptr, topk_ids ? topk_ids : x, ids_dtype}, lookup, n_experts,
                  num_slots, a_div, tile, counters, n_counters, partials, n_partials, stream);
+}
+
+extern "C" int bh_hex_moe_glu_ids_noalloc(const void* x, int32_t x_dtype, int64_t s_xm, void* act, int64_t s_am,
+                                          const bh_hex_proj* gate, const bh_hex_proj* up, int32_t bits,
+                                          int64_t n_out, int64_t n_in, const void* topk_ids, int32_t ids_dtype,
+                                          const int32_t* lookup, int32_t n_experts, int64_t num_slots, int32_t a_div,
+                                          const bh_hex_tile* tile, void* stream) {
+  const char* who = "bh_hex_moe_glu_ids_noalloc";
+  if (!topk_ids && num_slots > 0) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": null ids");
+  if (!tile) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": null tile");
+  if (tile->block_m != 16 && tile->block_m != 32 && tile->block_m != 64)
+    return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": block_m must be 16, 32 or 64");
+  if (num_slots < 0 || num_slots > kPlanMaxSlots || n_experts <= 0 || n_experts > kMaxExperts || n_out <= 0 ||
+      n_out > (1 << 30) || n_in <= 0 || n_in > (1 << 30))
+    return fail(BH_HEX_ERR_VALUE, std::string(who) + ": bad sizes (at most 1024 slots and 1024 experts)");
+  const int64_t nb = cdiv(num_slots, tile->block_m) + std::min<int64_t>(n_experts, num_slots);
+  const Workspace w = workspace_layout(nb, n_out, n_in, tile->block_m / 16, true);
+  if (w.counters > kScratchCounters || w.partials > kScratchPartials)
+    return fail(BH_HEX_ERR_UNSUPPORTED,
+                std::string(who) + ": the launch needs " + std::to_string(w.counters) + " counters and " +
+                    std::to_string(w.partials) + " partial sums; the static scratch holds " +
+                    std::to_string(kScratchCounters) + " and " + std::to_string(kScratchPartials) +
+                    " (use bh_hex_moe_glu_ids with a workspace)");
+  uint32_t* s = nullptr;
+  if (int rc = scratch_for(who, reinterpret_cast<hipStream_t>(stream), &s)) return rc;
+  return moe_glu(who, x, x_dtype, s_xm, act, s_am, gate, up, bits, n_out, n_in,
+                 PlanSrc{nullptr, nullptr, 0, nullptr, topk_ids ? topk_ids : x, ids_dtype}, lookup, n_experts,
+                 num_slots, a_div, tile, reinterpret_cast<int32_t*>(s), kScratchCounters,
+                 reinterpret_cast<float*>(s + kScratchCounters), kScratchPartials, stream);
 }
 
 extern "C" int bh_hex_moe_down(const void* act, int32_t act_dtype, int64_t s_am, void* y, int32_t y_dtype, int64_t s_ym,

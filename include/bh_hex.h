@@ -12,7 +12,8 @@
  *
  * Conventions for every entry point:
  *   - all pointers are device pointers (HIP), owned by the caller; the library keeps none of
- *     them after it returns and allocates no device memory;
+ *     them after it returns and allocates no device memory (bh_hex_moe_glu_ids_noalloc uses a
+ *     static device array of the library instead of a caller workspace);
  *   - strides are in elements; the innermost dimension of every tensor is contiguous;
  *   - work is enqueued on `stream` (a hipStream_t; NULL is the default stream) and nothing
  *     synchronises the host, so every entry point can be captured in a hipGraph;
@@ -31,7 +32,7 @@
 extern "C" {
 #endif
 
-#define BH_HEX_ABI_VERSION 8
+#define BH_HEX_ABI_VERSION 9
 
 enum bh_hex_status {
   BH_HEX_OK = 0,
@@ -175,6 +176,23 @@ int bh_hex_moe_glu_ids(const void* x, int32_t x_dtype, int64_t s_xm, void* act, 
                        const void* topk_ids, int32_t ids_dtype, const int32_t* lookup, int32_t n_experts,
                        int64_t num_slots, int32_t a_div, const bh_hex_tile* tile, int32_t* counters,
                        int64_t n_counters, float* partials, int64_t n_partials, void* stream);
+
+/* bh_hex_moe_glu_ids without a workspace argument: it allocates nothing and takes no caller
+ * workspace. No counterpart in the reference; it is for callers that cannot allocate device
+ * memory (code under hipGraph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Its counters and partial sums live in a static device array of this library (17 MiB per
+ * device, held until the process ends): 2^18 counters and 2^22 partial floats, enough for
+ * 16-slot blocks on every CU of an MI355X; a launch that needs more returns
+ * BH_HEX_ERR_UNSUPPORTED (bh_hex_moe_workspace gives the needs). The first call on a device
+ * looks the array up and clears its counters (a fill kernel on `stream`); every call leaves
+ * them zero. All calls on one device share the array: calls that overlap in time on one device
+ * (different streams, or different host threads) race. Same limits and results as
+ * bh_hex_moe_glu_ids. */
+int bh_hex_moe_glu_ids_noalloc(const void* x, int32_t x_dtype, int64_t s_xm, void* act, int64_t s_am,
+                               const bh_hex_proj* gate, const bh_hex_proj* up, int32_t bits, int64_t n_out,
+                               int64_t n_in, const void* topk_ids, int32_t ids_dtype, const int32_t* lookup,
+                               int32_t n_experts, int64_t num_slots, int32_t a_div, const bh_hex_tile* tile,
+                               void* stream);
 
 /* bh_hex_moe_down with the plan derived from the routing ids in the kernel, as
  * bh_hex_moe_glu_ids (same limits and workspace). Replaces the second _hex_moe_kernel launch of
