@@ -172,47 +172,69 @@ def event_time_ms(g, reps: int) -> float:
 
 
 def kernel_breakdown(cfg, copies, x, w, ids, reps):
-    """Average microseconds per launch of each kernel (graphs of one kernel kind over the copies)."""
+    """Average microseconds per launch of each kernel the layer runs (graphs of one kernel kind over
+    the copies), with the launches hex_moe_fused chooses: up to KERNEL_PLAN_MAX slots on the decode
+    kernels these sort the slots themselves (no plan launch), otherwise the align plan."""
     import torch
 
+    from blackhole_runtime import _lib
     from blackhole_runtime import hex_moe as hm
     T, k = ids.shape
     S = T * k
     E, H, I = cfg["E"], cfg["H"], cfg["I"]
     flat = ids.reshape(-1)
+    ids_flat, code = hm._ids_arg(flat)
     c1 = hm.default_config(S, I, H, True, E)
     c2 = hm.default_config(S, H, I, False, E)
     bm1 = hm._tile_from(c1)
     bm2 = hm._tile_from(c2)
+    own1 = bm1 != 128 and S <= hm.KERNEL_PLAN_MAX          # as hex_moe_fused (align_mode "auto")
+    own2 = bm2 != 128 and S <= hm.KERNEL_PLAN_MAX
     n_tiers = len(copies[0])
     lks = [t.lookup if n_tiers > 1 else None for t in copies[0]]     # per-tier plans, as hex_moe_fused
-    p1 = [hm.plan(flat, E, bm1, "auto", lk) for lk in lks]
-    p2 = [hm.plan(flat, E, bm2, "auto", lk) for lk in lks]
+    p1 = [None if own1 else hm.plan(flat, E, bm1, "auto", lk) for lk in lks]
+    p2 = [None if own2 else hm.plan(flat, E, bm2, "auto", lk) for lk in lks]
     act = torch.empty(S, I, dtype=x.dtype, device=x.device)
     y = torch.empty(S, H, dtype=x.dtype if bm2 == 128 else torch.float32, device=x.device)   # as hex_moe_fused
+    out = torch.empty(T, H, dtype=x.dtype, device=x.device)
     wf = w.reshape(-1).float().contiguous()
     res = {}
 
     def glu():
         for tiers in copies:
             for i, t in enumerate(tiers):
-                hm._launch_glu(x, act, t, *p1[i], S, k, bm1)
+                if own1:
+                    hm._launch_glu_ids(x, act, t, ids_flat, code, S, k, bm1)
+                else:
+                    hm._launch_glu(x, act, t, *p1[i], S, k, bm1)
 
     def down():
         for tiers in copies:
             for i, t in enumerate(tiers):
-                hm._launch_down(act, y, t, *p2[i], S, wf, bm2)
+                if own2:
+                    hm._launch_down_ids(act, y, t, ids_flat, code, S, wf, bm2)
+                else:
+                    hm._launch_down(act, y, t, *p2[i], S, wf, bm2)
 
     def plan():
         for _ in copies:
             for lk in lks:
                 hm.plan(flat, E, bm1, "auto", lk)
 
+    def reduce():
+        lib = _lib.load()
+        for _ in copies:
+            _lib.check(lib.bh_hex_moe_reduce(y.data_ptr(), _lib.dtype_code(y.dtype), y.stride(0), ids_flat.data_ptr(),
+                                             code, E, T, k, H, out.data_ptr(), _lib.dtype_code(out.dtype),
+                                             out.stride(0), _lib.stream_of(x)), "bh_hex_moe_reduce")
+
     n = len(copies)
     res["glu_us"] = event_time_ms(graph_of(glu), reps) * 1e3 / (n * n_tiers)
     res["down_us"] = event_time_ms(graph_of(down), reps) * 1e3 / (n * n_tiers)
-    res["plan_us"] = event_time_ms(graph_of(plan), reps) * 1e3 / n
-    res["tiles"] = {"glu": c1, "down": c2, "plan": "direct" if S <= hm.DIRECT_MAX else "align"}
+    res["plan_us"] = 0.0 if (own1 and own2) else event_time_ms(graph_of(plan), reps) * 1e3 / n
+    res["sum_us"] = event_time_ms(graph_of(reduce), reps) * 1e3 / n
+    res["tiles"] = {"glu": c1, "down": c2,
+                    "plan": "in-kernel" if (own1 and own2) else ("direct" if S <= hm.DIRECT_MAX else "align")}
     return res
 
 
@@ -349,6 +371,49 @@ def _short(name: str) -> str:
     return name.replace("bh::", "")[:110]
 
 
+def _kind(name: str) -> str:
+    """Role of a dispatch in the decode layer: gate/up, down, sum, plan or other."""
+    if "hex_moe_kernel<" in name:
+        return "gate/up" if name.split("hex_moe_kernel<", 1)[1].split(",")[2].strip() == "true" else "down"
+    if "moe_reduce_kernel" in name:
+        return "sum"
+    if "align" in name or "direct_kernel" in name:
+        return "plan"
+    return "other"
+
+
+def layer_sequence(trace: list) -> list[str]:
+    """The decode layer's dispatches as the timed graph replays them: every run of consecutive
+    dispatches [plan,] gate/up, down, sum on one queue; median duration of each kernel, the
+    median gap before it, and the median layer span (first start to last end)."""
+    import statistics
+    rows = sorted(((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), _kind(r["Kernel_Name"]), _short(r["Kernel_Name"]))
+                   for r in trace), key=lambda t: t[0])
+    layers = []
+    for i in range(len(rows) - 2):
+        if [rows[i + j][2] for j in range(3)] == ["gate/up", "down", "sum"]:
+            seq = rows[i - 1:i + 3] if i > 0 and rows[i - 1][2] == "plan" else rows[i:i + 3]
+            layers.append(seq)
+    if not layers:
+        return []
+    out = [f"## decode layer as replayed: {len(layers)} runs of [plan,] gate/up -> down -> sum",
+           f"{'kernel':<60} {'role':>8} {'n':>6} {'avg_us':>8} {'med_us':>8} {'gap_before_us':>14}"]
+    by = {}
+    for seq in layers:
+        for j, (st, en, kind, name) in enumerate(seq):
+            gap = (st - seq[j - 1][1]) / 1e3 if j else float("nan")
+            by.setdefault((kind, name), []).append(((en - st) / 1e3, gap))
+    for (kind, name), v in by.items():
+        d = [a for a, _ in v]
+        g = [b for _, b in v if b == b]
+        out.append(f"{name[:60]:<60} {kind:>8} {len(v):>6} {sum(d) / len(d):>8.2f} {statistics.median(d):>8.2f} "
+                   f"{(statistics.median(g) if g else float('nan')):>14.2f}")
+    spans = [(seq[-1][1] - seq[0][0]) / 1e3 for seq in layers]
+    out.append(f"layer span (first start to last end): median {statistics.median(spans):.2f} us, "
+               f"mean {sum(spans) / len(spans):.2f} us")
+    return out
+
+
 def rocprof_summary(dirs: list[str]) -> str:
     """Text summary of rocprofv3 CSV output directories: per-kernel dispatch statistics from a
     --kernel-trace --stats run, mean counter values per dispatch from --pmc runs, and, when a
@@ -357,6 +422,7 @@ def rocprof_summary(dirs: list[str]) -> str:
     (written to TRAFFIC_FILE)."""
     out, counters = [], {}
     for d in dirs:
+        out += layer_sequence(list(_csv_rows(d, "kernel_trace.csv")))
         stats = list(_csv_rows(d, "kernel_stats.csv"))
         if stats:
             out.append(f"## kernel statistics ({d})")
