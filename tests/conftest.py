@@ -12,7 +12,7 @@ from pathlib import Path
 import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
-for p in (ROOT, ROOT / "blackhole-harness_amd"):
+for p in (ROOT, ROOT / "blackhole-harness_amd", ROOT / "tests"):
     if str(p) not in sys.path:
         sys.path.insert(0, str(p))
 

@@ -13,6 +13,7 @@ import torch
 
 from blackhole_runtime import hex_moe as hm
 from blackhole_runtime import vllm_hex
+from fake_vllm import fake_vllm
 from oracle import hex_oracle as O
 
 
@@ -153,68 +154,8 @@ def test_assemble_tiers_checks():
         vllm_hex.assemble_tiers({}, (4, 64, 32), "l0")
 
 
-def _fake_vllm(monkeypatch):
-    registry = {}
-
-    def mod(name):
-        m = types.ModuleType(name)
-        monkeypatch.setitem(sys.modules, name, m)
-        return m
-
-    for name in ("vllm", "vllm.model_executor", "vllm.model_executor.layers"):
-        mod(name)
-    fm = mod("vllm.model_executor.layers.fused_moe")
-
-    class FusedMoEMethodBase:
-        def __init__(self, moe):
-            self.moe = moe
-
-    class RoutedExperts:
-        pass
-
-    fm.FusedMoEMethodBase, fm.RoutedExperts = FusedMoEMethodBase, RoutedExperts
-    lin = mod("vllm.model_executor.layers.linear")
-
-    class LinearBase:
-        pass
-
-    class UnquantizedLinearMethod:
-        pass
-
-    lin.LinearBase, lin.UnquantizedLinearMethod = LinearBase, UnquantizedLinearMethod
-    q = mod("vllm.model_executor.layers.quantization")
-
-    def register_quantization_config(name):
-        def deco(cls):
-            registry[name] = cls
-            return cls
-        return deco
-
-    q.register_quantization_config = register_quantization_config
-    bc = mod("vllm.model_executor.layers.quantization.base_config")
-
-    class QuantizationConfig:
-        pass
-
-    bc.QuantizationConfig = QuantizationConfig
-    ve = mod("vllm.model_executor.layers.vocab_parallel_embedding")
-
-    class UnquantizedEmbeddingMethod:
-        def process_weights_after_loading(self, layer):
-            pass
-
-        def apply(self, layer, x, bias=None):
-            return x @ layer.weight.T
-
-    class ParallelLMHead:
-        pass
-
-    ve.ParallelLMHead, ve.UnquantizedEmbeddingMethod = ParallelLMHead, UnquantizedEmbeddingMethod
-    return registry, RoutedExperts, ParallelLMHead, LinearBase
-
-
 def test_register_with_fake_vllm(monkeypatch):
-    registry, RoutedExperts, ParallelLMHead, LinearBase = _fake_vllm(monkeypatch)
+    registry, RoutedExperts, ParallelLMHead, LinearBase = fake_vllm(monkeypatch)
     vllm_hex.register()
     vllm_hex.register()                                       # idempotent
     cfg = registry[vllm_hex.NAME].from_config({"quant_method": "blackhole-hex", "head_ids": [1, 3]})
