@@ -39,9 +39,20 @@ class HexTile(ctypes.Structure):
     _fields_ = [("block_m", ctypes.c_int32), ("block_n", ctypes.c_int32), ("k_split", ctypes.c_int32)]
 
 
+class Routing(ctypes.Structure):
+    """struct bh_hex_routing."""
+    _fields_ = [("scoring", ctypes.c_int32), ("renormalize", ctypes.c_int32), ("n_group", ctypes.c_int32),
+                ("topk_group", ctypes.c_int32), ("routed_scaling_factor", ctypes.c_float),
+                ("correction_bias", ctypes.c_void_p)]
+
+
+# bh_hex_scoring
+SCORE_SOFTMAX, SCORE_SIGMOID = 0, 1
+
 _P, _I32, _I64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
 _PROJ = ctypes.POINTER(HexProj)
 _TILE = ctypes.POINTER(HexTile)
+_ROUTING = ctypes.POINTER(Routing)
 
 # name -> (restype, argtypes): every symbol include/bh_hex.h declares
 SIGNATURES = {
@@ -49,6 +60,10 @@ SIGNATURES = {
     "bh_hex_abi_version": (ctypes.c_int, []),
     "bh_hex_dequant": (ctypes.c_int, [_PROJ, _I32, _I64, _I64, _I64, _P, _P, _I32, _I64, _I64, _I64, _I32, _P]),
     "bh_hex_route_topk": (ctypes.c_int, [_P, _I32, _I64, _I64, _I32, _I32, _I32, _P, _P, _I32, _P]),
+    "bh_hex_route_select": (ctypes.c_int, [_P, _I32, _I64, _I64, _I32, _I32, _ROUTING, _P, _P, _I32, _P]),
+    "bh_hex_route_gemm": (ctypes.c_int, [_P, _I32, _I64, _P, _I64, _I64, _I32, _I32, _I32, _ROUTING, _P, _I64, _P, _P,
+                                         _I32, _P, _I64, _P]),
+    "bh_hex_route_gemm_workspace": (ctypes.c_int64, [_I64]),
     "bh_hex_align_max_blocks": (ctypes.c_int64, [_I64, _I32, _I32]),
     "bh_hex_align": (ctypes.c_int, [_P, _I32, _I64, _I32, _I32, _P, _P, _P, _P]),
     "bh_hex_align_tier": (ctypes.c_int, [_P, _I32, _I64, _I32, _P, _I32, _P, _P, _P, _P]),
@@ -70,7 +85,7 @@ SIGNATURES = {
     "bh_hex_moe_reduce": (ctypes.c_int, [_P, _I32, _I64, _P, _I32, _I32, _I64, _I32, _I64, _P, _I32, _I64, _P]),
 }
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _lib = None
 

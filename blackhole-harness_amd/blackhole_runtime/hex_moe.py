@@ -562,6 +562,85 @@ def hex_moe(x: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor,
 # --------------------------------------------------------------------------- routing
 
 
+def _routing(scoring: str, renormalize: bool, n_group: int, topk_group: int, correction_bias, scale: float, E: int,
+             device) -> tuple:
+    """The bh_hex_routing struct of the options (and the bias tensor it points to)."""
+    if scoring not in ("softmax", "sigmoid"):
+        raise ValueError(f"scoring must be 'softmax' or 'sigmoid', got {scoring!r}")
+    bias = None
+    if correction_bias is not None:
+        if correction_bias.device != device and torch.cuda.is_current_stream_capturing():
+            raise ValueError("correction_bias must be on the GPU when the routing is captured in a graph "
+                             "(a host tensor would be copied during capture)")
+        bias = correction_bias.to(device=device, dtype=torch.float32).reshape(-1).contiguous()
+        if bias.numel() != E:
+            raise ValueError(f"correction_bias has {bias.numel()} values for {E} experts")
+    r = _lib.Routing(_lib.SCORE_SIGMOID if scoring == "sigmoid" else _lib.SCORE_SOFTMAX, int(renormalize), int(n_group),
+                     int(topk_group), float(scale), None if bias is None else bias.data_ptr())
+    return r, bias
+
+
+def route_select(logits: torch.Tensor, k: int, scoring: str = "softmax", renormalize: bool = True, n_group: int = 1,
+                 topk_group: int = 0, correction_bias: torch.Tensor | None = None,
+                 routed_scaling_factor: float = 1.0, ids_dtype: torch.dtype = torch.int64
+                 ) -> tuple[torch.Tensor, torch.Tensor]:
+    """Expert choice from router logits [T, E] on the GPU (reaper/reaper_pipeline/moe.py:141-168,
+    route_from_logits): softmax top-k, or sigmoid scores plus correction_bias for the choice,
+    group-limited by n_group / topk_group, unbiased weights; renormalised, then scaled.
+    (weights float32 [T, k] in descending order of choice, ids [T, k])."""
+    lib = _lib.load()
+    _lib.require_gpu(logits)
+    if logits.stride(-1) != 1:
+        logits = logits.contiguous()
+    T, E = logits.shape
+    r, bias = _routing(scoring, renormalize, n_group, topk_group, correction_bias, routed_scaling_factor, E,
+                       logits.device)
+    w = torch.empty(T, k, dtype=torch.float32, device=logits.device)
+    ids = torch.empty(T, k, dtype=ids_dtype, device=logits.device)
+    _lib.check(lib.bh_hex_route_select(logits.data_ptr(), _lib.dtype_code(logits.dtype), logits.stride(0), T, E, k,
+                                       r, w.data_ptr(), ids.data_ptr(), _lib.dtype_code(ids_dtype),
+                                       _lib.stream_of(logits)), "bh_hex_route_select")
+    return w, ids
+
+
+def route(x: torch.Tensor, router_weight: torch.Tensor, k: int, scoring: str = "softmax", renormalize: bool = True,
+          n_group: int = 1, topk_group: int = 0, correction_bias: torch.Tensor | None = None,
+          routed_scaling_factor: float = 1.0, ids_dtype: torch.dtype = torch.int64
+          ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Router logits x [T, H] @ router_weight [E, H]^T (the MoE block's gate linear, bf16/f16,
+    rounded to x.dtype) and the expert choice of route_select, in one launch (bh_hex_route_gemm).
+    Returns (weights float32 [T, k], ids [T, k], logits float32 [T, E])."""
+    lib = _lib.load()
+    _lib.require_gpu(x, router_weight)
+    if x.dtype not in (torch.bfloat16, torch.float16) or router_weight.dtype != x.dtype:
+        raise NotImplementedError("route takes bf16 or f16 activations and a router weight of the same dtype")
+    x = x if x.stride(-1) == 1 and x.stride(0) % 8 == 0 else x.contiguous()
+    wr = router_weight if router_weight.stride(-1) == 1 and router_weight.stride(0) % 8 == 0 else router_weight.contiguous()
+    T, H = x.shape
+    E = wr.shape[0]
+    if wr.shape[1] != H:
+        raise ValueError(f"router weight {tuple(wr.shape)} does not match hidden size {H}")
+    r, bias = _routing(scoring, renormalize, n_group, topk_group, correction_bias, routed_scaling_factor, E, x.device)
+    w = torch.empty(T, k, dtype=torch.float32, device=x.device)
+    ids = torch.empty(T, k, dtype=ids_dtype, device=x.device)
+    logits = torch.empty(T, E, dtype=torch.float32, device=x.device)
+    cnt, _ = _kept_workspace("route", x.device, max(1, lib.bh_hex_route_gemm_workspace(T)), 0, 0)
+    _lib.check(lib.bh_hex_route_gemm(x.data_ptr(), _lib.dtype_code(x.dtype), x.stride(0), wr.data_ptr(), wr.stride(0),
+                                     T, H, E, k, r, logits.data_ptr(), logits.stride(0), w.data_ptr(), ids.data_ptr(),
+                                     _lib.dtype_code(ids_dtype), cnt.data_ptr(), cnt.numel(), _lib.stream_of(x)),
+               "bh_hex_route_gemm")
+    return w, ids, logits
+
+
+def moe_layer(x: torch.Tensor, router_weight: torch.Tensor, tiers: list[HexTier], k: int, **routing) -> torch.Tensor:
+    """A routed-expert MoE layer from its router weight: route (router logits and expert choice,
+    one launch), then hex_moe on the chosen experts. routing: route()'s options (scoring,
+    renormalize, n_group, topk_group, correction_bias, routed_scaling_factor). The shared experts
+    are not applied (as in the reference's plugin path, vllm_hex.py:145-146)."""
+    w, ids, _ = route(x, router_weight, k, **routing)
+    return hex_moe(x, w, ids, tiers)
+
+
 def route_topk(logits: torch.Tensor, k: int, renormalize: bool = True,
                ids_dtype: torch.dtype = torch.int64) -> tuple[torch.Tensor, torch.Tensor]:
     """Softmax routing on the GPU (reaper/reaper_pipeline/moe.py:161-166, softmax branch):

@@ -1,7 +1,5 @@
-// Routing and slot planning for the HEX MoE kernels.
+// Slot planning for the HEX MoE kernels (the routing itself is in hex_router.hip).
 //
-//   bh_hex_route_topk  softmax -> top-k -> renormalise, one wave per token
-//                      (reaper/reaper_pipeline/moe.py:161-166, softmax branch)
 //   bh_hex_align       stable counting sort of slots by expert, padded to block_m
 //                      (runtime/blackhole_runtime/hex_moe.py:201-222)
 //   bh_hex_direct      one block per slot (hex_moe.py:228-237)
@@ -17,88 +15,6 @@
 #include "hex_common.h"
 
 namespace bh {
-
-// ----------------------------------------------------------------------------------- top-k
-
-template <int LDT>
-__device__ __forceinline__ float load_logit(const void* p, int64_t i) {
-  if constexpr (LDT == BH_HEX_F32) return reinterpret_cast<const float*>(p)[i];
-  else if constexpr (LDT == BH_HEX_BF16) return bf16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
-  else return f16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
-}
-
-constexpr int kTopkPerLane = 16;   // up to 1024 experts
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
-  return v;
-}
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
-  return v;
-}
-
-template <int LDT, int IDT>
-__global__ __launch_bounds__(256) void route_topk_kernel(const void* __restrict__ logits, int64_t s_lt, int64_t T,
-                                                         int32_t E, int32_t k, int32_t renorm,
-                                                         float* __restrict__ topk_w, void* __restrict__ topk_ids) {
-  const int lane = threadIdx.x & 63;
-  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= T) return;
-  float p[kTopkPerLane];
-  float mx = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < kTopkPerLane; ++j) {
-    const int e = lane + kWave * j;
-    p[j] = e < E ? load_logit<LDT>(logits, t * s_lt + e) : -INFINITY;
-    mx = fmaxf(mx, p[j]);
-  }
-  mx = wave_max(mx);
-  float s = 0.f;
-#pragma unroll
-  for (int j = 0; j < kTopkPerLane; ++j) {
-    const int e = lane + kWave * j;
-    p[j] = e < E ? expf(p[j] - mx) : 0.f;
-    s += p[j];
-  }
-  s = wave_sum(s);
-#pragma unroll
-  for (int j = 0; j < kTopkPerLane; ++j) {
-    const int e = lane + kWave * j;
-    p[j] = e < E ? p[j] / s : -1.f;      // probabilities; -1 never wins
-  }
-  float wsel = 0.f, wsum = 0.f;
-  int isel = 0;
-  for (int r = 0; r < k; ++r) {
-    // this lane's best (largest value, then lowest expert id)
-    float bv = -2.f;
-    int bi = 0x7FFFFFFF;
-#pragma unroll
-    for (int j = 0; j < kTopkPerLane; ++j) {
-      const int e = lane + kWave * j;
-      if (p[j] > bv) { bv = p[j]; bi = e; }
-    }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-      const float ov = __shfl_xor(bv, m, kWave);
-      const int oi = __shfl_xor(bi, m, kWave);
-      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-    }
-#pragma unroll
-    for (int j = 0; j < kTopkPerLane; ++j)
-      if (lane + kWave * j == bi) p[j] = -2.f;
-    wsum += bv;
-    if (lane == r) { wsel = bv; isel = bi; }
-  }
-  if (lane < k) {
-    const float w = renorm ? wsel / wsum : wsel;
-    topk_w[t * k + lane] = w;
-    if constexpr (IDT == BH_HEX_I64) reinterpret_cast<int64_t*>(topk_ids)[t * k + lane] = isel;
-    else reinterpret_cast<int32_t*>(topk_ids)[t * k + lane] = isel;
-  }
-}
 
 // ----------------------------------------------------------------------------------- align
 
@@ -385,34 +301,6 @@ __global__ __launch_bounds__(256) void direct_kernel(const void* __restrict__ id
 }  // namespace bh
 
 using namespace bh;
-
-extern "C" int bh_hex_route_topk(const void* logits, int32_t logits_dtype, int64_t s_lt, int64_t T, int32_t E, int32_t k,
-                                 int32_t renormalize, float* topk_w, void* topk_ids, int32_t ids_dtype, void* stream) {
-  if (T < 0) return fail(BH_HEX_ERR_VALUE, "bh_hex_route_topk: negative token count");
-  if (E <= 0 || E > kWave * kTopkPerLane)
-    return fail(BH_HEX_ERR_UNSUPPORTED, "bh_hex_route_topk: experts must be in 1.." + std::to_string(kWave * kTopkPerLane));
-  if (k <= 0 || k > E || k > kWave) return fail(BH_HEX_ERR_VALUE, "bh_hex_route_topk: k must be in 1..min(E, 64)");
-  if (ids_dtype != BH_HEX_I32 && ids_dtype != BH_HEX_I64)
-    return fail(BH_HEX_ERR_UNSUPPORTED, "bh_hex_route_topk: ids dtype must be I32 or I64");
-  if (T == 0) return BH_HEX_OK;
-  if (!logits || !topk_w || !topk_ids) return fail(BH_HEX_ERR_VALUE, "bh_hex_route_topk: null pointer");
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const dim3 grid((unsigned)cdiv(T, 4));
-#define BH_ROUTE(LDT, IDT)                                                                                         \
-  hipLaunchKernelGGL((route_topk_kernel<LDT, IDT>), grid, dim3(256), 0, st, logits, s_lt, T, E, k, renormalize, topk_w, \
-                     topk_ids)
-  if (logits_dtype == BH_HEX_F32) {
-    if (ids_dtype == BH_HEX_I64) BH_ROUTE(BH_HEX_F32, BH_HEX_I64); else BH_ROUTE(BH_HEX_F32, BH_HEX_I32);
-  } else if (logits_dtype == BH_HEX_BF16) {
-    if (ids_dtype == BH_HEX_I64) BH_ROUTE(BH_HEX_BF16, BH_HEX_I64); else BH_ROUTE(BH_HEX_BF16, BH_HEX_I32);
-  } else if (logits_dtype == BH_HEX_F16) {
-    if (ids_dtype == BH_HEX_I64) BH_ROUTE(BH_HEX_F16, BH_HEX_I64); else BH_ROUTE(BH_HEX_F16, BH_HEX_I32);
-  } else {
-    return fail(BH_HEX_ERR_UNSUPPORTED, "bh_hex_route_topk: logits dtype must be F32, BF16 or F16");
-  }
-#undef BH_ROUTE
-  return check_launch("bh_hex_route_topk");
-}
 
 extern "C" int64_t bh_hex_align_max_blocks(int64_t S, int32_t n_experts, int32_t block_m) {
   if (block_m <= 0 || S < 0 || n_experts < 0) return -1;

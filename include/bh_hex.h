@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define BH_HEX_ABI_VERSION 9
+#define BH_HEX_ABI_VERSION 10
 
 enum bh_hex_status {
   BH_HEX_OK = 0,
@@ -96,6 +96,47 @@ int bh_hex_dequant(const bh_hex_proj* w, int32_t bits, int64_t n, int64_t n_out,
  * (softmax branch), as vLLM computes it before HexMoEMethod.apply (vllm_hex.py:239-240). */
 int bh_hex_route_topk(const void* logits, int32_t logits_dtype, int64_t s_lt, int64_t T, int32_t E, int32_t k,
                       int32_t renormalize, float* topk_w, void* topk_ids, int32_t ids_dtype, void* stream);
+
+/* Expert choice from router logits, as reaper/reaper_pipeline/moe.py:141-168 (route_from_logits)
+ * states it for the models the reference serves:
+ *   softmax branch: p = softmax(logits); the k largest p; divided by their sum if renormalize;
+ *   sigmoid branch (scoring BH_HEX_SCORE_SIGMOID, or any correction_bias): s = sigmoid(logits),
+ *     choice = s + correction_bias[e]; with n_group > 1 the experts form n_group groups of
+ *     E / n_group consecutive ids, each group scores the sum of its two largest choices, only the
+ *     topk_group best groups keep their experts (0: every group); the k largest choices; their
+ *     weights are the unbiased s, divided by (their sum + 1e-20) if renormalize;
+ *   then every weight times routed_scaling_factor.
+ * Ties go to the lower expert (or group) id. Weights in descending order of choice. */
+enum bh_hex_scoring { BH_HEX_SCORE_SOFTMAX = 0, BH_HEX_SCORE_SIGMOID = 1 };
+typedef struct bh_hex_routing {
+  int32_t scoring;                /* bh_hex_scoring                                          */
+  int32_t renormalize;            /* norm_topk_prob                                          */
+  int32_t n_group;                /* 1: no groups; at most 64, dividing E into groups of >= 2 */
+  int32_t topk_group;             /* groups kept, 0..n_group (0: all)                        */
+  float routed_scaling_factor;    /* 1.0 for none                                            */
+  const float* correction_bias;   /* device float [E] or null (e_score_correction_bias)      */
+} bh_hex_routing;
+
+/* The choice above for logits [T, E] (F32, BF16 or F16; row stride s_lt): topk_w float [T, k],
+ * topk_ids [T, k] in ids_dtype (I32 or I64). routing null: softmax, renormalised, no scaling.
+ * E <= 1024, k <= min(E, 64). What vLLM's expert selection computes before
+ * HexMoEMethod.apply (reaper/reaper_pipeline/moe.py:141-168). */
+int bh_hex_route_select(const void* logits, int32_t logits_dtype, int64_t s_lt, int64_t T, int32_t E, int32_t k,
+                        const bh_hex_routing* routing, float* topk_w, void* topk_ids, int32_t ids_dtype, void* stream);
+
+/* Router logits and expert choice in one launch: logits[t, e] = sum_h x[t, h] w_router[e, h]
+ * (the MoE block's gate linear, no bias) accumulated in float32 on the matrix cores, rounded to
+ * x_dtype (BF16 or F16, the gate linear's output dtype) and written as float32 to logits
+ * [T, E] (row stride s_lt), then the choice of bh_hex_route_select on them. x [T, H] and
+ * w_router [E, H] in x_dtype with 16-byte aligned rows; H a multiple of 32. counters: int32
+ * workspace of bh_hex_route_gemm_workspace(T) values, zero before the first call and left zero
+ * by every call; calls sharing it must not overlap in time. Replaces the gate linear
+ * (reaper/reaper_pipeline/moe.py:141, the router module) and the choice after it. */
+int bh_hex_route_gemm(const void* x, int32_t x_dtype, int64_t s_xm, const void* w_router, int64_t s_we, int64_t T,
+                      int32_t H, int32_t E, int32_t k, const bh_hex_routing* routing, float* logits, int64_t s_lt,
+                      float* topk_w, void* topk_ids, int32_t ids_dtype, int32_t* counters, int64_t n_counters,
+                      void* stream);
+int64_t bh_hex_route_gemm_workspace(int64_t T);
 
 /* Number of expert blocks align() produces: ceil(S / block_m) + min(n_experts, S). */
 int64_t bh_hex_align_max_blocks(int64_t S, int32_t n_experts, int32_t block_m);

@@ -26,6 +26,15 @@ What pins each function (tests/test_oracle.py):
   align / direct    invariants of runtime/tests/test_hex_moe.py:47-61 plus an independent
                     pure-Python sequential construction; the reference's worked example.
   route_topk        torch.softmax + torch.topk (an independent implementation).
+  route_select      properties that a dropped term or a wrong branch breaks: the softmax branch
+                    equals route_topk; sigmoid ids equal softmax ids (both monotone in the
+                    logits) without bias or groups; weights are the unbiased scores of the chosen
+                    ids and sum to the scaling factor when renormalised; a correction bias that
+                    strongly favours k experts selects exactly them; groups: n_group = 1 or
+                    topk_group = n_group change nothing, and the kept groups equal a pure-Python
+                    brute force over every group's top-2 sum; the reference's toy Kimi gate
+                    (reaper/tests/test_pipeline_moe.py:196-211) restated in torch.
+  router_logits     float64 products rounded once (a pure-Python dot product on small cases).
   moe_reference     float64 brute force (per-token, per-slot loops) on tiny shapes.
   quantize          golden fixtures written from the reference quantizer in
                     tests/golden/make_golden.py (blackhole.anatomy.hex.quantize).
@@ -241,6 +250,64 @@ def route_topk(logits, k: int, renormalize: bool = True):
     if renormalize:
         w = w / w.sum(-1, keepdims=True)
     return w.astype(np.float32), ids.astype(np.int64)
+
+
+def _topk_desc(v: np.ndarray, k: int) -> np.ndarray:
+    """Indices of the k largest values of each row, in descending order, ties to the lower index."""
+    return np.argsort(-v, axis=-1, kind="stable")[..., :k]
+
+
+def route_select(logits, k: int, scoring: str = "softmax", renormalize: bool = True, n_group: int = 1,
+                 topk_group: int = 0, correction_bias=None, routed_scaling_factor: float = 1.0):
+    """Expert choice from router logits [T, E] (reaper/reaper_pipeline/moe.py:141-168,
+    route_from_logits), in float32:
+      sigmoid branch (taken when a correction bias is given or scoring == "sigmoid"):
+        scores = sigmoid(logits); choice = scores + bias; with n_group > 1 each group of E/n_group
+        consecutive experts scores the sum of its two largest choices, only the topk_group best
+        groups stay (0: all), the others' choices are -inf; ids = the k largest choices, weights =
+        their unbiased scores, divided by (their sum + 1e-20) when renormalize;
+      softmax branch: probabilities, the k largest, divided by their sum when renormalize;
+    then weights * routed_scaling_factor. Ties go to the lower expert / group id.
+    Returns (weights float32 [T, k], ids int64 [T, k])."""
+    lg = np.asarray(logits, np.float32)
+    T, E = lg.shape
+    if correction_bias is not None or scoring == "sigmoid":
+        scores = (np.float32(1.0) / (np.float32(1.0) + np.exp(-lg))).astype(np.float32)
+        choice = scores + np.asarray(correction_bias, np.float32) if correction_bias is not None else scores.copy()
+        if n_group > 1:
+            G = E // n_group
+            grp = np.sort(choice.reshape(T, n_group, G), axis=-1)[..., ::-1]
+            gs = (grp[..., 0] + grp[..., 1]).astype(np.float32)
+            keep = _topk_desc(gs, topk_group or n_group)
+            mask = np.zeros((T, n_group), bool)
+            np.put_along_axis(mask, keep, True, axis=-1)
+            choice = np.where(np.repeat(mask, G, axis=-1), choice, np.float32(-np.inf))
+        ids = _topk_desc(choice, k)
+        w = np.take_along_axis(scores, ids, -1)
+        if renormalize:
+            w = w / (w.sum(-1, keepdims=True, dtype=np.float32) + np.float32(1e-20))
+    else:
+        m = lg.max(-1, keepdims=True)
+        ex = np.exp(lg - m)
+        p = (ex / ex.sum(-1, keepdims=True)).astype(np.float32)
+        ids = _topk_desc(p, k)
+        w = np.take_along_axis(p, ids, -1)
+        if renormalize:
+            w = w / w.sum(-1, keepdims=True, dtype=np.float32)
+    w = (w * np.float32(routed_scaling_factor)).astype(np.float32)
+    return w, ids.astype(np.int64)
+
+
+def router_logits(x, w_router, round_to: str | None = "bf16") -> np.ndarray:
+    """Router logits [T, E] = x [T, H] @ w_router [E, H]^T (the model's gate linear, no bias),
+    accumulated in float64 and rounded to the activation dtype (round_to "bf16" / "f16" / None for
+    float32), as a bf16 gate linear hands them to the routing."""
+    acc = np.asarray(x, np.float64) @ np.asarray(w_router, np.float64).T
+    if round_to == "bf16":
+        return bf16_round(acc.astype(np.float32))
+    if round_to == "f16":
+        return acc.astype(np.float16).astype(np.float32)
+    return acc.astype(np.float32)
 
 
 # --------------------------------------------------------------------------- the MoE layer

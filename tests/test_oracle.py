@@ -6,6 +6,7 @@ vectors written from the reference quantizer)."""
 from __future__ import annotations
 
 import hashlib
+import math
 import sys
 from pathlib import Path
 
@@ -352,3 +353,100 @@ def test_random_parts_ranges():
     assert p["idx"].shape == (4, 8, 6) and p["block_scale"].min() >= 40 and p["block_scale"].max() < 70
     assert np.all(np.diff(p["levels"], axis=-1) >= 0) and np.all(np.abs(p["levels"]) <= 1)
     assert np.all((p["expert_scale"] >= 0.01) & (p["expert_scale"] <= 0.03))
+
+
+# --------------------------------------------------------------------------- routing from logits
+
+
+def _logits(T, E, seed):
+    return np.random.default_rng(seed).standard_normal((T, E)).astype(np.float32)
+
+
+def test_route_select_softmax_branch_is_route_topk():
+    lg = _logits(32, 96, 1)
+    for renorm in (True, False):
+        w, ids = O.route_select(lg, 8, renormalize=renorm)
+        w2, ids2 = O.route_topk(lg, 8, renorm)
+        assert np.array_equal(ids, ids2)
+        np.testing.assert_allclose(w, w2, rtol=1e-6)
+
+
+def test_route_select_sigmoid_properties():
+    lg = _logits(64, 96, 2)
+    k = 8
+    # sigmoid and softmax are both monotone in the logits: the same experts, in the same order
+    w, ids = O.route_select(lg, k, "sigmoid", renormalize=False)
+    assert np.array_equal(ids, O.route_select(lg, k)[1])
+    sig = 1.0 / (1.0 + np.exp(-lg.astype(np.float64)))
+    np.testing.assert_allclose(w, np.take_along_axis(sig, ids, -1), rtol=1e-6)
+    # renormalised weights sum to the scaling factor
+    w, _ = O.route_select(lg, k, "sigmoid", routed_scaling_factor=2.5)
+    np.testing.assert_allclose(w.sum(-1), 2.5, rtol=1e-5)
+    # a correction bias that strongly favours k experts picks exactly them; the weights stay the
+    # unbiased scores of those experts
+    fav = np.array([3, 17, 40, 41, 60, 77, 90, 95])
+    bias = np.zeros(96, np.float32)
+    bias[fav] = 10.0
+    w, ids = O.route_select(lg, k, correction_bias=bias, renormalize=False)
+    assert all(sorted(r) == sorted(fav.tolist()) for r in ids.tolist())
+    np.testing.assert_allclose(w, np.take_along_axis(sig, ids, -1), rtol=1e-6)
+    # the bias alone switches to the sigmoid branch (scoring left at "softmax")
+    assert np.array_equal(O.route_select(lg, k, correction_bias=np.zeros(96))[1], O.route_select(lg, k, "sigmoid")[1])
+
+
+def _groups_brute(choice_row, n_group, topk_group, k):
+    """Pure-Python group-limited top-k of one token."""
+    E = len(choice_row)
+    G = E // n_group
+    gs = []
+    for q in range(n_group):
+        vals = sorted((float(v) for v in choice_row[q * G:(q + 1) * G]), reverse=True)
+        gs.append((-(np.float32(vals[0]) + np.float32(vals[1])), q))
+    kept = {q for _, q in sorted(gs)[:topk_group]}
+    cand = sorted((-float(choice_row[e]), e) for e in range(E) if e // G in kept)
+    return [e for _, e in cand[:k]]
+
+
+def test_route_select_groups():
+    lg = _logits(40, 64, 3)
+    bias = (np.random.default_rng(4).standard_normal(64) * 0.3).astype(np.float32)
+    k = 6
+    base = O.route_select(lg, k, "sigmoid", correction_bias=bias)
+    assert np.array_equal(O.route_select(lg, k, "sigmoid", n_group=1, correction_bias=bias)[1], base[1])
+    assert np.array_equal(O.route_select(lg, k, "sigmoid", n_group=8, topk_group=8, correction_bias=bias)[1], base[1])
+    for n_group, topk_group in ((8, 3), (4, 2), (16, 5)):
+        w, ids = O.route_select(lg, k, "sigmoid", n_group=n_group, topk_group=topk_group, correction_bias=bias)
+        choice = (1.0 / (1.0 + np.exp(-lg))).astype(np.float32) + bias
+        for t in range(lg.shape[0]):
+            assert ids[t].tolist() == _groups_brute(choice[t], n_group, topk_group, k), (n_group, t)
+
+
+def test_route_select_kimi_toy_gate():
+    """The reference test's DeepSeek-V3 style gate (reaper/tests/test_pipeline_moe.py:196-211),
+    restated in torch: sigmoid scores, correction bias for the choice only, renormalised and scaled."""
+    import torch
+    g = torch.Generator().manual_seed(0)
+    E, H, k, scale = 6, 16, 2, 2.0
+    weight = torch.randn(E, H, generator=g)
+    bias = torch.randn(E, generator=g) * 0.3
+    x = torch.randn(15, H, generator=g)
+    s = torch.nn.functional.linear(x, weight).sigmoid()
+    idx = (s + bias).topk(k, dim=-1)[1]
+    w = s.gather(1, idx)
+    w = w / w.sum(-1, keepdim=True) * scale
+    logits = torch.nn.functional.linear(x, weight).numpy()
+    w2, ids2 = O.route_select(logits, k, correction_bias=bias.numpy(), routed_scaling_factor=scale)
+    assert np.array_equal(ids2, idx.numpy())
+    np.testing.assert_allclose(w2, w.numpy(), rtol=2e-6)
+
+
+def test_router_logits_dot_products():
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((3, 40)).astype(np.float32)
+    W = rng.standard_normal((5, 40)).astype(np.float32)
+    got = O.router_logits(x, W, None)
+    for t in range(3):
+        for e in range(5):
+            acc = math.fsum(float(x[t, i]) * float(W[e, i]) for i in range(40))
+            assert got[t, e] == np.float32(acc)
+    assert np.array_equal(O.router_logits(x, W, "bf16"), O.bf16_round(got))
