@@ -182,6 +182,13 @@ def kernel_breakdown(cfg, copies, x, w, ids, reps):
     T, k = ids.shape
     S = T * k
     E, H, I = cfg["E"], cfg["H"], cfg["I"]
+    if len(copies[0]) == 1 and 0 < S <= hm.GEMV_MAX and hm.gemv_fits(k, H, I):
+        # hex_moe_fused runs the layer as the two matrix-vector launches of one call
+        def gemv():
+            for tiers in copies:
+                hm.hex_moe_gemv(x, w, ids, tiers[0])
+        return {"gemv_us": event_time_ms(graph_of(gemv), reps) * 1e3 / len(copies),
+                "tiles": {"path": "matrix-vector: bh_hex_moe_gemv (gate/up, then down with the k-slot sum)"}}
     flat = ids.reshape(-1)
     ids_flat, code = hm._ids_arg(flat)
     c1 = hm.default_config(S, I, H, True, E)
@@ -375,6 +382,10 @@ def _kind(name: str) -> str:
     """Role of a dispatch in the decode layer: gate/up, down, sum, plan or other."""
     if "hex_moe_kernel<" in name:
         return "gate/up" if name.split("hex_moe_kernel<", 1)[1].split(",")[2].strip() == "true" else "down"
+    if "gemv_glu_kernel" in name:
+        return "gate/up"
+    if "gemv_down_kernel" in name:
+        return "down"
     if "moe_reduce_kernel" in name:
         return "sum"
     if "align" in name or "direct_kernel" in name:
@@ -384,19 +395,26 @@ def _kind(name: str) -> str:
 
 def layer_sequence(trace: list) -> list[str]:
     """The decode layer's dispatches as the timed graph replays them: every run of consecutive
-    dispatches [plan,] gate/up, down, sum on one queue; median duration of each kernel, the
-    median gap before it, and the median layer span (first start to last end)."""
+    dispatches [plan,] gate/up, down[, sum] on one queue (the matrix-vector launches add the
+    k-slot sum inside down); median duration of each kernel, the median gap before it, the median
+    layer span (first start to last end) and the median period between consecutive layers."""
     import statistics
     rows = sorted(((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), _kind(r["Kernel_Name"]), _short(r["Kernel_Name"]))
                    for r in trace), key=lambda t: t[0])
     layers = []
-    for i in range(len(rows) - 2):
-        if [rows[i + j][2] for j in range(3)] == ["gate/up", "down", "sum"]:
-            seq = rows[i - 1:i + 3] if i > 0 and rows[i - 1][2] == "plan" else rows[i:i + 3]
-            layers.append(seq)
+    i = 0
+    while i < len(rows) - 1:
+        if rows[i][2] == "gate/up" and rows[i + 1][2] == "down":
+            end = i + 3 if i + 2 < len(rows) and rows[i + 2][2] == "sum" else i + 2
+            start = i - 1 if i > 0 and rows[i - 1][2] == "plan" else i
+            layers.append(rows[start:end])
+            i = end
+        else:
+            i += 1
     if not layers:
         return []
-    out = [f"## decode layer as replayed: {len(layers)} runs of [plan,] gate/up -> down -> sum",
+    kinds = " -> ".join(k for _, _, k, _ in layers[len(layers) // 2])
+    out = [f"## decode layer as replayed: {len(layers)} runs of {kinds}",
            f"{'kernel':<60} {'role':>8} {'n':>6} {'avg_us':>8} {'med_us':>8} {'gap_before_us':>14}"]
     by = {}
     for seq in layers:
@@ -409,8 +427,11 @@ def layer_sequence(trace: list) -> list[str]:
         out.append(f"{name[:60]:<60} {kind:>8} {len(v):>6} {sum(d) / len(d):>8.2f} {statistics.median(d):>8.2f} "
                    f"{(statistics.median(g) if g else float('nan')):>14.2f}")
     spans = [(seq[-1][1] - seq[0][0]) / 1e3 for seq in layers]
+    periods = [(b[0][0] - a[0][0]) / 1e3 for a, b in zip(layers, layers[1:])]
     out.append(f"layer span (first start to last end): median {statistics.median(spans):.2f} us, "
                f"mean {sum(spans) / len(spans):.2f} us")
+    if periods:
+        out.append(f"layer period (start to the next layer's start): median {statistics.median(periods):.2f} us")
     return out
 
 
@@ -523,15 +544,22 @@ def main(argv=None) -> int:
         f"{head['hbm_gbps']:.0f} GB/s, kernels {head['kernels']}")
 
     k = head["kernels"]
-    glu_gbs = head["glu_bytes"] / (k["glu_us"] * 1e-6) / 1e9
     traffic, traffic_src = None, None
-    if a.config == 2 and T == 16 and a.block == 128 and TRAFFIC_FILE.exists():
-        traffic = json.loads(TRAFFIC_FILE.read_text())["traffic_bytes"]
-        traffic_src = str(TRAFFIC_FILE.relative_to(ROOT))
-    roofline = {"bound": "hbm", "achieved": glu_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": glu_gbs / HBM_PEAK_GBS, "traffic": traffic, "traffic_source": traffic_src,
-                "kernel": f"{GLU_KERNEL} (gate/up + SiLU)", "algorithmic_bytes_per_launch": head["glu_bytes"],
-                "avg_launch_us": k["glu_us"]}
+    if "glu_us" in k:
+        glu_gbs = head["glu_bytes"] / (k["glu_us"] * 1e-6) / 1e9
+        if a.config == 2 and T == 16 and a.block == 128 and TRAFFIC_FILE.exists():
+            traffic = json.loads(TRAFFIC_FILE.read_text())["traffic_bytes"]
+            traffic_src = str(TRAFFIC_FILE.relative_to(ROOT))
+        roofline = {"bound": "hbm", "achieved": glu_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": glu_gbs / HBM_PEAK_GBS, "traffic": traffic, "traffic_source": traffic_src,
+                    "kernel": f"{GLU_KERNEL} (gate/up + SiLU)", "algorithmic_bytes_per_launch": head["glu_bytes"],
+                    "avg_launch_us": k["glu_us"]}
+    else:   # the matrix-vector launches: the layer's bytes over the two launches' time
+        gbs = head["layer_bytes"] / (k["gemv_us"] * 1e-6) / 1e9
+        roofline = {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": gbs / HBM_PEAK_GBS, "traffic": None, "traffic_source": None,
+                    "kernel": "gemv_glu_kernel + gemv_down_kernel (the whole layer)",
+                    "algorithmic_bytes_per_launch": head["layer_bytes"], "avg_launch_us": k["gemv_us"]}
 
     sweep = {}
     roofline_prefill = None

@@ -51,6 +51,12 @@ SPLIT = int(os.environ.get("BLACKHOLE_HEX_SPLIT", "2"))
 # slots up to which the decode kernels sort the slots by expert themselves (bh_hex_moe_*_ids), so
 # no align launch precedes them (at most 1024; 0 always launches the align kernel)
 KERNEL_PLAN_MAX = min(1024, int(os.environ.get("BLACKHOLE_HEX_KERNEL_PLAN_MAX", "1024")))
+# slots up to which a single tier's layer runs as two matrix-vector launches (bh_hex_moe_gemv:
+# no plan, no workspace, the k-slot sum inside the down launch); 0 never. Measured against the
+# expert-block kernels (layer us, top-8): config 2 widths T=1 13.6 vs 38.8, T=4 26.5 vs 48.4,
+# T=8 44.0 vs 60.2, T=12 68.0 vs 58.2; hidden 4096 / 1536 wide experts T=4 76.6 vs 92.6, T=6 110.9
+# vs 104.6. The gap closes as slots share experts (each slot reads its expert's weights).
+GEMV_MAX = int(os.environ.get("BLACKHOLE_HEX_GEMV_MAX", "32"))
 
 
 def _n_in(p: dict, bits: int) -> int:
@@ -380,6 +386,42 @@ def _launch_down_ids(act, y, t: HexTier, ids, code, S, w, bm):
         tile, cnt.data_ptr(), cnt.numel(), part.data_ptr(), part.numel(), _lib.stream_of(act)), "bh_hex_moe_down_ids")
 
 
+def gemv_fits(k: int, H: int, I: int) -> bool:
+    """Whether bh_hex_moe_gemv takes a layer of these widths (its limits in include/bh_hex.h)."""
+    return 0 < k <= 16 and H % HEX_BLOCK == 0 and I % HEX_BLOCK == 0 and H <= 4096 and I <= 2048
+
+
+def hex_moe_gemv(x, topk_weights, topk_ids, tier: HexTier) -> torch.Tensor:
+    """Routed-expert output [T, H] in x.dtype of one tier for a few tokens, as two matrix-vector
+    launches (bh_hex_moe_gemv): gate/up for every slot, then down with the top-k weights and the
+    k-slot sum (hex_moe.py:304-325 for such batches). Slots whose expert is not in the tier
+    contribute nothing. Reads each routed expert's weights once per slot routed to it."""
+    _lib.require_gpu(x, topk_weights, topk_ids)
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise NotImplementedError(f"the matrix-vector launches take bf16 or f16 activations, got {x.dtype}")
+    T, k = topk_ids.shape
+    H = x.shape[1]
+    I = tier.gate_proj["idx"].shape[1]
+    assert H == _n_in(tier.gate_proj, tier.bits), f"input width {H} != HEX width {_n_in(tier.gate_proj, tier.bits)}"
+    if not gemv_fits(k, H, I):
+        raise NotImplementedError(f"bh_hex_moe_gemv takes k <= 16, hidden <= 4096 and inter <= 2048 "
+                                  f"(multiples of 32): got k={k}, hidden={H}, inter={I}")
+    x = x.contiguous()
+    out = torch.empty(T, H, dtype=x.dtype, device=x.device)
+    if T == 0:
+        return out
+    ids, code = _ids_arg(topk_ids)
+    w = topk_weights.reshape(-1).float().contiguous()
+    act = torch.empty(T * k, I, dtype=x.dtype, device=x.device)
+    lib = _lib.load()
+    dt = _lib.dtype_code(x.dtype)
+    _lib.check(lib.bh_hex_moe_gemv(
+        x.data_ptr(), dt, x.stride(0), act.data_ptr(), act.stride(0), out.data_ptr(), dt, out.stride(0),
+        tier.struct("gate_proj"), tier.struct("up_proj"), tier.struct("down_proj"), tier.bits, H, I, ids.data_ptr(),
+        code, w.data_ptr(), tier.lookup.data_ptr(), tier.lookup.numel(), T, k, _lib.stream_of(x)), "bh_hex_moe_gemv")
+    return out
+
+
 def _covers_all(tiers: list[HexTier]) -> bool:
     """Whether every expert id has a tier (then every slot's y row is written by a kernel)."""
     seen: set = set()
@@ -405,6 +447,9 @@ def hex_moe_fused(x, topk_weights, topk_ids, tiers: list[HexTier], config: dict 
     H = x.shape[1]
     I = tiers[0].gate_proj["idx"].shape[1]
     E = tiers[0].lookup.numel()
+    if (len(tiers) == 1 and config is None and align_mode == "auto" and 0 < S <= GEMV_MAX
+            and gemv_fits(k, H, I)):
+        return hex_moe_gemv(x, topk_weights, topk_ids, tiers[0])
     x = x.contiguous()
     out = torch.empty(T, H, dtype=x.dtype, device=x.device)
     if T == 0:

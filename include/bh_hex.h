@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define BH_HEX_ABI_VERSION 10
+#define BH_HEX_ABI_VERSION 11
 
 enum bh_hex_status {
   BH_HEX_OK = 0,
@@ -264,6 +264,27 @@ int bh_hex_moe_workspace(int64_t num_blocks, int64_t n_out, int64_t n_in, int32_
 int bh_hex_moe_reduce(const void* y, int32_t y_dtype, int64_t s_ym, const void* topk_ids, int32_t ids_dtype,
                       int32_t n_experts, int64_t T, int32_t k, int64_t H, void* out, int32_t out_dtype, int64_t s_ot,
                       void* stream);
+
+/* The whole layer of one tier for a few tokens, as two matrix-vector launches (no plan, no
+ * workspace): act[s, o] as bh_hex_moe_glu writes it for every slot s < T * k whose expert has
+ * this tier (one wave per slot and output row; act [T * k, inter], row stride s_am, in x_dtype,
+ * rows of other slots left unwritten), then
+ *   out[t, h] = sum_j topk_w[t * k + j] * es_d * sum_i act[t * k + j, i] W_d[h, i]
+ * over the token's slots of this tier, in float32, rounded once to out_dtype (= x_dtype): the
+ * down projection, the top-k weight and the k-slot sum in one launch (one wave per token and
+ * output row). Slots whose id (topk_ids, I32 or I64) is outside [0, n_experts) or has no
+ * expert in this tier (lookup[id] < 0) contribute nothing. Weights enter as in bh_hex_moe_glu
+ * (round(level) times activations in float32, each 32-input block's partial times its fp8
+ * scale, the expert scale at the end). Limits: k <= 16, hidden <= 4096, inter <= 2048, widths
+ * multiples of 32, T * k <= 65535; otherwise BH_HEX_ERR_UNSUPPORTED. Each weight row of
+ * a routed expert is read once per slot that routes to it, so the launches suit batches of a few
+ * tokens. Replaces, for such batches, align, the two _hex_moe_kernel launches and the sum of
+ * hex_moe_fused (hex_moe.py:304-325). */
+int bh_hex_moe_gemv(const void* x, int32_t x_dtype, int64_t s_xm, void* act, int64_t s_am, void* out,
+                    int32_t out_dtype, int64_t s_om, const bh_hex_proj* gate, const bh_hex_proj* up,
+                    const bh_hex_proj* down, int32_t bits, int64_t hidden, int64_t inter, const void* topk_ids,
+                    int32_t ids_dtype, const float* topk_w, const int32_t* lookup, int32_t n_experts, int64_t T,
+                    int32_t k, void* stream);
 
 #ifdef __cplusplus
 }

@@ -66,7 +66,7 @@ SHAPES = [
 
 
 @pytest.mark.parametrize("name,E,H,I,k,groups,T,zipf", SHAPES, ids=[s[0] for s in SHAPES])
-def test_full_shape_layer(name, E, H, I, k, groups, T, zipf):
+def test_full_shape_layer(name, E, H, I, k, groups, T, zipf, monkeypatch):
     say(f"full shape {name}: E={E} H={H} I={I} k={k} tiers={groups} T={T}")
     block = 128
     g = torch.Generator(device=DEV).manual_seed(E + T)
@@ -99,10 +99,19 @@ def test_full_shape_layer(name, E, H, I, k, groups, T, zipf):
         # path="auto" keeps to the fused kernels at every batch unless BLACKHOLE_HEX_DEQUANT_MIN
         # is set (the fused results do not depend on timing, so they are equal bit for bit)
         assert torch.equal(hm.hex_moe(x, w, ids, tiers), fused)
+    blocks = fused
+    if len(tiers) == 1 and T * k <= hm.GEMV_MAX and hm.gemv_fits(k, H, I):
+        # the layer ran as the two matrix-vector launches; now through the expert-block kernels
+        monkeypatch.setattr(hm, "GEMV_MAX", 0)
+        blocks = hm.hex_moe_fused(x, w, ids, tiers)
+        err = rel_err(blocks, want)
+        say(f"  expert-block kernels: {err:.2e}")
+        assert err < TOL_16, err
+        monkeypatch.undo()
     if T * k <= hm.KERNEL_PLAN_MAX:
         # the kernels' own slot plan equals the align kernel's (align_mode "vllm" maps to the align
         # kernel at every batch), so the outputs are equal bit for bit
-        assert torch.equal(hm.hex_moe_fused(x, w, ids, tiers, align_mode="vllm"), fused)
+        assert torch.equal(hm.hex_moe_fused(x, w, ids, tiers, align_mode="vllm"), blocks)
     if T * k <= hm.DIRECT_MAX:
         # the reference's direct plan (one block per slot) at full width
         err = rel_err(hm.hex_moe_fused(x, w, ids, tiers, align_mode="direct"), want)

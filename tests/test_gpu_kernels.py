@@ -563,7 +563,7 @@ def test_workspace_kept_alive_when_it_grows():
         w, ids = routing(T, E, k, seed=seed)
         x = torch.randn(T, H, generator=torch.Generator().manual_seed(seed)).to(torch.bfloat16).to(DEV)
         return x, torch.from_numpy(w).to(DEV), torch.from_numpy(ids).to(DEV)
-    xs, ws_, ids_s = inputs(2, 61)          # 8 slots: a small workspace
+    xs, ws_, ids_s = inputs(hm.GEMV_MAX // k + 1, 61)   # past the matrix-vector path: a small workspace
     xb, wb, idb = inputs(64, 62)            # 256 slots on 32-slot blocks: a larger one
     with torch.cuda.stream(s):
         eager = hm.hex_moe_fused(xs, ws_, ids_s, tiers)
