@@ -222,9 +222,11 @@ __device__ __forceinline__ void glu_row_dot(const GluRow<IT>& r, const GemvArgs&
   }
 }
 
-// Grid (row groups, slots): workgroup g of slot s covers rows g * 16 + wave, then every
+// Grid (row groups, slots): workgroup g of slot s covers rows g * 16 + wave, then (LOOP) every
 // gridDim.x * 16 rows after it, each wave requesting its next row before it computes the current.
-template <int BITS, int ADT, int IT>
+// Without LOOP a wave computes one row and holds one row's weights (fewer registers, so more
+// waves resident: for grids that fit the GPU in one round).
+template <int BITS, int ADT, int IT, bool LOOP>
 __global__ __launch_bounds__(kGvGluWaves * kWave) void gemv_glu_kernel(GemvArgs a) {
   constexpr int L = 1 << BITS, NP = L * L, C = 1 << kGvGluCs, NT = kGvGluWaves * kWave;
   static_assert(NP * C / 4 <= NT && kGvMaxH / 8 <= NT, "four copies of an entry and one activation piece per thread");
@@ -260,11 +262,10 @@ __global__ __launch_bounds__(kGvGluWaves * kWave) void gemv_glu_kernel(GemvArgs 
   const __amdgpu_buffer_rsrc_t ru = buffer_rsrc(a.u.idx + (int64_t)e * a.u.s_ie, (int64_t)a.I * a.u.s_in * 4);
   const __amdgpu_buffer_rsrc_t rbg = buffer_rsrc(a.g.block_scale + (int64_t)e * a.g.s_be, (int64_t)a.I * a.g.s_bn);
   const __amdgpu_buffer_rsrc_t rbu = buffer_rsrc(a.u.block_scale + (int64_t)e * a.u.s_be, (int64_t)a.I * a.u.s_bn);
-  // two row buffers, both requested before the barrier: a wave computes row n while the next
-  // row's weights are in flight, then requests the row after that into the freed buffer
+  // two row buffers: a wave requests row n + stride before it computes row n (the first row
+  // alone before the barrier: more requests ahead of the table loads delay the tables)
   GluRow<IT> r0, r1;
   glu_row_load<BITS, IT>(r0, a, rg, ru, rbg, rbu, n, lane, nb);
-  glu_row_load<BITS, IT>(r1, a, rg, ru, rbg, rbu, n + stride, lane, nb);
   if (has_entry) {
     const uint32_t g = to_bits<ADT>(lv[0]) | (to_bits<ADT>(lv[1]) << 16);
     const uint32_t u = to_bits<ADT>(lv[2]) | (to_bits<ADT>(lv[3]) << 16);
@@ -274,13 +275,17 @@ __global__ __launch_bounds__(kGvGluWaves * kWave) void gemv_glu_kernel(GemvArgs 
   if (has_x) xs[piece_slot(tid, nb)] = xv;
   __syncthreads();
   const float esg = a.g.expert_scale[e], esu = a.u.expert_scale[e];
+  if constexpr (!LOOP) {
+    if (n < a.I) glu_row_dot<BITS, ADT, IT>(r0, a, tab[0], tab[1], xs, s, n, lane, nb, esg, esu);
+    return;
+  }
   while (n < a.I) {                     // (wave-uniform; no barrier inside)
+    glu_row_load<BITS, IT>(r1, a, rg, ru, rbg, rbu, n + stride, lane, nb);
     glu_row_dot<BITS, ADT, IT>(r0, a, tab[0], tab[1], xs, s, n, lane, nb, esg, esu);
-    glu_row_load<BITS, IT>(r0, a, rg, ru, rbg, rbu, n + 2 * stride, lane, nb);
     n += stride;
     if (n >= a.I) break;
+    glu_row_load<BITS, IT>(r0, a, rg, ru, rbg, rbu, n + stride, lane, nb);
     glu_row_dot<BITS, ADT, IT>(r1, a, tab[0], tab[1], xs, s, n, lane, nb, esg, esu);
-    glu_row_load<BITS, IT>(r1, a, rg, ru, rbg, rbu, n + 2 * stride, lane, nb);
     n += stride;
   }
 }
@@ -405,17 +410,27 @@ static unsigned glu_groups(int resident, const GemvArgs& a) {
   return (unsigned)cdiv(rows, per);
 }
 
+// Workgroups of a kernel that one CU holds at once.
+template <typename K>
+static int resident_of(K kernel) {
+  int r = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&r, kernel, kGvGluWaves * kWave, 0) != hipSuccess || r < 1) r = 1;
+  return r;
+}
+
+// One row per wave when every row's wave fits the GPU at once; otherwise waves walk rows.
 template <int BITS, int ADT, int IT>
 static void glu_launch(hipStream_t st, const GemvArgs& a) {
-  auto kernel = gemv_glu_kernel<BITS, ADT, IT>;
-  static int resident = 0;              // workgroups of this kernel one CU holds
-  if (resident == 0) {
-    int r = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&r, kernel, kGvGluWaves * kWave, 0) != hipSuccess || r < 1) r = 1;
-    resident = r;
+  static const int res_one = resident_of(gemv_glu_kernel<BITS, ADT, IT, false>);
+  static const int res_loop = resident_of(gemv_glu_kernel<BITS, ADT, IT, true>);
+  const int64_t groups = cdiv(a.I, kGvGluWaves);
+  if (groups * a.T * a.k <= (int64_t)device_cus() * res_one) {
+    const dim3 grid((unsigned)groups, (unsigned)(a.T * a.k));
+    hipLaunchKernelGGL((gemv_glu_kernel<BITS, ADT, IT, false>), grid, dim3(kGvGluWaves * kWave), 0, st, a);
+  } else {
+    const dim3 grid(glu_groups(res_loop, a), (unsigned)(a.T * a.k));
+    hipLaunchKernelGGL((gemv_glu_kernel<BITS, ADT, IT, true>), grid, dim3(kGvGluWaves * kWave), 0, st, a);
   }
-  const dim3 grid(glu_groups(resident, a), (unsigned)(a.T * a.k));
-  hipLaunchKernelGGL(kernel, grid, dim3(kGvGluWaves * kWave), 0, st, a);
 }
 
 template <int BITS, int ADT, int GS>
