@@ -281,6 +281,11 @@ def run_layer(cfg, copies, T, steps, warmup, block, breakdown=True):
            "layer_bytes": total, "hbm_gbps": total / (ms * 1e-3) / 1e9,
            "hbm_frac": total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
            "mfma_frac": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, "glu_bytes": glu_b}
+    if T == 1:
+        # the reference's one-token figure (hex_check.py:121,136): top-k routed experts x 3 x H x I
+        # at 4.25 bits per weight (3.25 for a 3-bit tier), over the layer time
+        bpw = sum(len(t._experts_host) * (t.bits + 0.25) for t in copies[0]) / cfg["E"]
+        out["ref_t1_hex_weight_gbps"] = cfg["k"] * 3 * cfg["H"] * cfg["I"] * bpw / 8 / (ms * 1e-3) / 1e9
     if breakdown:
         out["kernels"] = kernel_breakdown(cfg, copies, x, w, ids, max(5, steps // (2 * n)))
     return out, (x, w, ids, logits)
@@ -567,7 +572,7 @@ def main(argv=None) -> int:
         for Ts in (1, 4, 64):
             r, _ = run_layer(cfg, copies, Ts, max(80, a.steps // 4), a.warmup, a.block, breakdown=False)
             sweep[f"T{Ts}"] = {kk: r[kk] for kk in ("ms_per_step", "tokens_per_s", "hbm_gbps", "hbm_frac",
-                                                     "unique_experts")}
+                                                     "unique_experts", "ref_t1_hex_weight_gbps") if kk in r}
             log(f"  T={Ts}: {r['ms_per_step'] * 1e3:.1f} us/layer, {r['hbm_gbps']:.0f} GB/s")
         del copies
         torch.cuda.empty_cache()
@@ -577,7 +582,7 @@ def main(argv=None) -> int:
             layers = build_tiers(CONFIGS[c], a.block, n_copies, dev)
             for Ts in batches:
                 r, _ = run_layer(CONFIGS[c], layers, Ts, steps, a.warmup, a.block, breakdown=c == 3)
-                sweep[f"config{c}_T{Ts}"] = {kk: r[kk] for kk in keys}
+                sweep[f"config{c}_T{Ts}"] = {kk: r[kk] for kk in keys + ("ref_t1_hex_weight_gbps",) if kk in r}
                 if c == 3:
                     roofline_prefill = prefill_roofline(CONFIGS[c], Ts, r["kernels"])
                 log(f"  config{c} T={Ts}: {r['ms_per_step'] * 1e3:.1f} us/layer, {r['hbm_gbps']:.0f} GB/s "

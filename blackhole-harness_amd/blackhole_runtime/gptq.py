@@ -19,18 +19,23 @@ and each expert's input Hessian H [n, in, in] (the sum of x x^T over the tokens 
              (harness/blackhole_pipeline/pack.py:53-86, 104-110)
 
 The arithmetic (float32 sweeps, float64 factorisations, the order of every reduction on the
-CPU) follows those files so that, on CPU tensors, the parts equal the reference's bit for bit;
-on the GPU the k-means sums run as atomics and float32 division is not correctly rounded, so
-scales and levels can differ in the last bits and a code can flip where a value sits within
-rounding of a midpoint. The GPU's batched float64 Cholesky has returned wrong factors with a
-success code here, so every device factorisation is checked by its residual and the failing
-problems are factorised again on the CPU.
+CPU) follows those files so that, on CPU tensors, the parts equal the reference's bit for bit.
+On device tensors the column sweep and the table indices run in this library's HIP kernel
+(bh_hex_gptq_sweep, one lane per weight row), which repeats the CPU's arithmetic operation for
+operation: on the same factor, levels and scales its Q and indices equal the reference's bit for
+bit. The header, k-means and factorisations stay torch on the device; there the k-means sums run
+as atomics and torch's float32 division is not correctly rounded, so scales and levels can differ
+in the last bits and a code can flip where a value sits within rounding of a midpoint. The GPU's
+batched float64 Cholesky has returned wrong factors with a success code here, so every device
+factorisation is checked by its residual and the failing problems are factorised again on the
+CPU.
 """
 
 from __future__ import annotations
 
 import torch
 
+from . import _lib
 from .quant import FP8_MAX, HEX_BLOCK, pack
 
 
@@ -165,6 +170,34 @@ def gptq_sweep(W: torch.Tensor, U: torch.Tensor, round_col, block: int = 128) ->
 
 
 @torch.no_grad()
+def sweep_device(W: torch.Tensor, U: torch.Tensor, levels: torch.Tensor, block_scale: torch.Tensor,
+                 scale_block: int = HEX_BLOCK, dead: torch.Tensor | None = None, block: int = 128):
+    """The GPTQ sweep and the table indices on the GPU (bh_hex_gptq_sweep): W [n, out, in] with
+    dead columns zeroed, U [n, in, in] the upper factor, levels [n, L] sorted, block_scale
+    [n, out, in / scale_block] the dequant scales, dead [n, in] bool or None. Returns (Q float32
+    [n, out, in] with dead columns zeroed, codes uint8 [n, out, in]), equal to gptq_sweep +
+    nearest_index on the CPU bit for bit."""
+    _lib.require_gpu(W, U, levels, block_scale, dead)
+    n, out, inp = W.shape
+    L = levels.shape[-1]
+    w = W.float().contiguous().clone()
+    u = U.float().contiguous()
+    lev = levels.float().contiguous()
+    sc = block_scale.float().contiguous()
+    if sc.shape != (n, out, inp // scale_block) or u.shape != (n, inp, inp) or lev.shape != (n, L):
+        raise ValueError(f"shapes: W {tuple(W.shape)}, U {tuple(u.shape)}, levels {tuple(lev.shape)}, "
+                         f"block_scale {tuple(sc.shape)} (scale block {scale_block})")
+    d = dead.to(torch.uint8).contiguous() if dead is not None else None
+    q = torch.empty_like(w)
+    codes = torch.empty(w.shape, dtype=torch.uint8, device=w.device)
+    lib = _lib.load()
+    _lib.check(lib.bh_hex_gptq_sweep(w.data_ptr(), u.data_ptr(), lev.data_ptr(), L, sc.data_ptr(), scale_block,
+                                     d.data_ptr() if d is not None else None, n, out, inp, block, q.data_ptr(),
+                                     codes.data_ptr(), _lib.stream_of(w)), "bh_hex_gptq_sweep")
+    return q, codes
+
+
+@torch.no_grad()
 def quantize_experts_gptq(W: torch.Tensor, H: torch.Tensor, L: int = 16, block: int = HEX_BLOCK,
                           damp: float = 0.01, sweep_block: int = 128) -> dict:
     """HEX parts of W [n, out, in] with GPTQ rounding under the Hessians H [n, in, in]:
@@ -189,8 +222,11 @@ def quantize_experts_gptq(W: torch.Tensor, H: torch.Tensor, L: int = 16, block: 
         return torch.gather(levels, 1, nearest_index((x / s).clamp(-1, 1), levels).reshape(n, -1)).view(x.shape) * s
 
     Wd, U, dead = hessian_factor(W, H, damp)
-    Q = gptq_sweep(Wd, U, round_col, sweep_block) * (~dead)[:, None, :]
-    codes = nearest_index((Q / scale).clamp(-1, 1), levels)
+    if W.is_cuda:
+        Q, codes = sweep_device(Wd, U, levels, blk[..., 0], block, dead, sweep_block)
+    else:
+        Q = gptq_sweep(Wd, U, round_col, sweep_block) * (~dead)[:, None, :]
+        codes = nearest_index((Q / scale).clamp(-1, 1), levels)
     es_w = (W.float().abs().amax(dim=(1, 2)) / FP8_MAX).clamp(min=1e-30)
     bs = (blk[..., 0] / es_w[:, None, None]).clamp(max=FP8_MAX).to(torch.float8_e4m3fn).view(torch.uint8)
     return {"idx": pack(codes, bits), "block_scale": bs.contiguous(), "expert_scale": es_w.float().contiguous(),

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define BH_HEX_ABI_VERSION 11
+#define BH_HEX_ABI_VERSION 12
 
 enum bh_hex_status {
   BH_HEX_OK = 0,
@@ -285,6 +285,24 @@ int bh_hex_moe_gemv(const void* x, int32_t x_dtype, int64_t s_xm, void* act, int
                     const bh_hex_proj* down, int32_t bits, int64_t hidden, int64_t inter, const void* topk_ids,
                     int32_t ids_dtype, const float* topk_w, const int32_t* lookup, int32_t n_experts, int64_t T,
                     int32_t k, void* stream);
+
+/* The GPTQ column sweep of the HEX producer, rounding onto each expert's level table, with the
+ * table indices of the result: for each of n experts, w [n, out, in] float32 (the weights with dead
+ * columns zeroed; overwritten: the sweep updates it), u [n, in, in] float32 the upper Cholesky
+ * factor of the damped inverse Hessian, levels [n, n_levels] float32 sorted (8 or 16), scale
+ * [n, out, in / scale_block] float32 the dequant scale of each scale block. Columns run in order in
+ * sweep blocks of `block` (1..128): column c of a row is rounded to the level nearest to
+ * clamp(w / s, -1, 1) (midpoints (a + b) / 2, a left search) times s; its error (w - q) / u[c, c]
+ * updates the block's later columns (w -= err * u[c, c'], product and difference each rounded)
+ * and, when the block ends, the later columns take w -= sum_k err_k u[k, c'] as one fused
+ * multiply-add chain over the block in column order. Then q is multiplied by 0 in the columns
+ * that dead [n, in] marks (null: none) and codes [n, out, in] (uint8) get the index of the level
+ * nearest to clamp(q / s, -1, 1). Every operation is the reference's on the CPU, so q and codes
+ * equal its output bit for bit on the same inputs. Replaces the sweep of
+ * reaper/gpu_perf/gptq.py:62-83 (_solve) and table_indices (harness/blackhole_pipeline/pack.py:53-62). */
+int bh_hex_gptq_sweep(float* w, const float* u, const float* levels, int32_t n_levels, const float* scale,
+                      int32_t scale_block, const uint8_t* dead, int64_t n, int64_t out, int64_t in, int32_t block,
+                      float* q, uint8_t* codes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,9 +1,17 @@
-"""The HEX producer with GPTQ rounding on the GPU (marked gpu): on the golden cases the expert
-scales agree to 2 ulp (the device's float32 division is not correctly rounded), at least 99.9% of
-the fp8 block codes and 99% of the indices agree, the levels agree to float32 rounding (the
-k-means sums run as atomics there) and the layer error under the Hessian is within 1% of the
-reference's; on a config-2-width stack (4 experts, 768 x 2048)
-GPTQ's layer error is below plain rounding's, and the parts run through the fused kernels."""
+"""The HEX producer with GPTQ rounding on the GPU (marked gpu).
+
+The column sweep and the table indices run in the HIP kernel bh_hex_gptq_sweep. Given the
+reference's own header scales, levels and Hessian factor (computed on the CPU, where they equal
+the reference's bit for bit), its Q and packed indices equal the golden vectors the reference
+wrote, bit for bit; on multi-block shapes (lazy updates of later blocks, tail chunks, partial
+waves, 8 and 16 levels, other scale and sweep blocks, dead columns) it equals the CPU sweep bit
+for bit. The whole producer on the device (torch header, k-means and factorisations around the
+kernel): the expert scales agree to 2 ulp (torch's float32 division on the device is not
+correctly rounded), at least 99.9% of the fp8 block codes and 99% of the indices agree, the
+levels agree to float32 rounding (the k-means sums run as atomics there) and the layer error
+under the Hessian is within 1% of the reference's; on a config-2-width stack (4 experts,
+768 x 2048) GPTQ's layer error is below plain rounding's, and the parts run through the fused
+kernels."""
 
 from __future__ import annotations
 
@@ -52,6 +60,68 @@ def test_gptq_on_gpu_matches_reference(case):
     e_got = layer_err(Wt, got["q"].cpu(), Ht)
     e_ref = layer_err(Wt, torch.from_numpy(GOLD[f"{name}__q"]), Ht)
     assert torch.all(e_got <= e_ref * 1.01 + 1e-12), (e_got, e_ref)
+
+
+def _cpu_inputs(W, H, L, block=32):
+    """The sweep's inputs as the reference forms them, on the CPU: (W with dead columns zeroed,
+    upper factor U, dead mask, block scales [n, out, in / block], levels)."""
+    xn, blk, _ = gptq.block_headers(W, block)
+    n, out, inp = W.shape
+    cw = H.diagonal(dim1=-2, dim2=-1).float().view(n, 1, inp // block, block)
+    wt = (cw.expand(n, out, -1, -1) * blk.pow(2)).reshape(n, -1)
+    levels = gptq.fit_levels(xn.reshape(n, -1), wt, L).contiguous().float()
+    Wd, U, dead = gptq.hessian_factor(W, H)
+    return Wd, U, dead, blk[..., 0].contiguous(), levels
+
+
+@pytest.mark.parametrize("case", G.CASES, ids=[c[0] for c in G.CASES])
+def test_sweep_kernel_bit_exact_on_golden(case):
+    name, n, o, i, L, tokens, seed = case
+    say(f"gptq sweep kernel, golden case {name}")
+    W, H = G.make_case(name, n, o, i, tokens, seed)
+    Wd, U, dead, bs, levels = _cpu_inputs(torch.from_numpy(W), torch.from_numpy(H), L)
+    assert torch.equal(levels, torch.from_numpy(GOLD[f"{name}__levels"]))
+    q, codes = gptq.sweep_device(Wd.to(DEV), U.to(DEV), levels.to(DEV), bs.to(DEV), 32, dead.to(DEV))
+    assert np.array_equal(q.cpu().numpy().view(np.uint32), GOLD[f"{name}__q"].view(np.uint32))
+    bits = L.bit_length() - 1
+    from blackhole_runtime.quant import pack
+    assert np.array_equal(pack(codes.cpu(), bits).numpy(), GOLD[f"{name}__idx"])
+
+
+@pytest.mark.parametrize("n,o,i,L,sblock,block", [(2, 70, 352, 16, 32, 128), (3, 64, 256, 8, 32, 128),
+                                                  (1, 130, 192, 16, 64, 64), (2, 5, 160, 8, 32, 100)])
+def test_sweep_kernel_equals_cpu_sweep(n, o, i, L, sblock, block):
+    say(f"gptq sweep kernel vs the CPU sweep n={n} out={o} in={i} L={L} sblock={sblock} block={block}")
+    g = torch.Generator().manual_seed(o + i)
+    W = torch.randn(n, o, i, generator=g) * 0.02
+    X = torch.randn(n, 3 * i, i, generator=g)
+    X[:, :, 3] *= 8.0
+    H = X.transpose(1, 2).contiguous() @ X
+    W[0, :, 9] = 0.0                                       # a dead column
+    Wd, U, dead, bs, levels = _cpu_inputs(W, H, L, sblock)
+    scale = bs[..., None].expand(-1, -1, -1, sblock).reshape(n, o, i)
+
+    def round_col(x, c):
+        s = scale[..., c:c + 1]
+        return torch.gather(levels, 1, gptq.nearest_index((x / s).clamp(-1, 1), levels).reshape(n, -1)).view(x.shape) * s
+    Q = gptq.gptq_sweep(Wd.clone(), U, round_col, block) * (~dead)[:, None, :]
+    codes = gptq.nearest_index((Q / scale).clamp(-1, 1), levels)
+    q_d, c_d = gptq.sweep_device(Wd.to(DEV), U.to(DEV), levels.to(DEV), bs.to(DEV), sblock, dead.to(DEV), block)
+    assert np.array_equal(q_d.cpu().numpy().view(np.uint32), Q.numpy().view(np.uint32))
+    assert torch.equal(c_d.cpu().long(), codes)
+
+
+def test_sweep_kernel_argument_checks():
+    say("gptq sweep kernel argument checks")
+    z = torch.zeros(1, 4, 64, device=DEV)
+    with pytest.raises(ValueError, match="shapes"):
+        gptq.sweep_device(z, torch.zeros(1, 64, 64, device=DEV), torch.zeros(1, 16, device=DEV),
+                          torch.ones(1, 4, 3, device=DEV))
+    with pytest.raises(NotImplementedError, match="8 or 16 levels"):
+        gptq.sweep_device(z, torch.zeros(1, 64, 64, device=DEV), torch.zeros(1, 4, device=DEV),
+                          torch.ones(1, 4, 2, device=DEV))
+    with pytest.raises(ValueError, match="on the GPU"):
+        gptq.sweep_device(z.cpu(), torch.zeros(1, 64, 64), torch.zeros(1, 16), torch.ones(1, 4, 2))
 
 
 def test_gptq_config2_width_and_fused_kernels():
