@@ -83,12 +83,14 @@ SIGNATURES = {
     "bh_hex_moe_workspace": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, ctypes.POINTER(ctypes.c_int64),
                                             ctypes.POINTER(ctypes.c_int64)]),
     "bh_hex_moe_reduce": (ctypes.c_int, [_P, _I32, _I64, _P, _I32, _I32, _I64, _I32, _I64, _P, _I32, _I64, _P]),
+    "bh_hex_block_header": (ctypes.c_int, [_P, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P, _P, _P]),
+    "bh_hex_fit_levels": (ctypes.c_int, [_P, _P, _I64, _I64, _I32, _P, _P, _P, _I32, _P, _P]),
     "bh_hex_gptq_sweep": (ctypes.c_int, [_P, _P, _P, _I32, _P, _I32, _P, _I64, _I64, _I64, _I32, _P, _P, _P]),
     "bh_hex_moe_gemv": (ctypes.c_int, [_P, _I32, _I64, _P, _I64, _P, _I32, _I64, _PROJ, _PROJ, _PROJ, _I32, _I64, _I64,
                                        _P, _I32, _P, _P, _I32, _I64, _I32, _P]),
 }
 
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 _lib = None
 

@@ -20,15 +20,16 @@ and each expert's input Hessian H [n, in, in] (the sum of x x^T over the tokens 
 
 The arithmetic (float32 sweeps, float64 factorisations, the order of every reduction on the
 CPU) follows those files so that, on CPU tensors, the parts equal the reference's bit for bit.
-On device tensors the column sweep and the table indices run in this library's HIP kernel
-(bh_hex_gptq_sweep, one lane per weight row), which repeats the CPU's arithmetic operation for
-operation: on the same factor, levels and scales its Q and indices equal the reference's bit for
-bit. The header, k-means and factorisations stay torch on the device; there the k-means sums run
-as atomics and torch's float32 division is not correctly rounded, so scales and levels can differ
-in the last bits and a code can flip where a value sits within rounding of a midpoint. The GPU's
-batched float64 Cholesky has returned wrong factors with a success code here, so every device
-factorisation is checked by its residual and the failing problems are factorised again on the
-CPU.
+On device tensors the block header (bh_hex_block_header), the k-means (bh_hex_fit_levels, each
+level's sums in sample order as the CPU's scatter_add) and the column sweep with the table indices
+(bh_hex_gptq_sweep, one lane per weight row) run in this library's HIP kernels, which repeat the
+CPU's arithmetic operation for operation (IEEE divides, the same products and sums in the same
+order, the CPU matrix product's fused multiply-add chain): on the same inputs they equal the
+reference's outputs bit for bit. The damped Hessian factorisations stay torch float64 on the
+device; their float32 cast equals the CPU's except where a value sits within float64 rounding of a
+float32 midpoint. The GPU's batched float64 Cholesky has returned wrong factors with a success code
+here, so every device factorisation is checked by its residual and the failing problems are
+factorised again on the CPU.
 """
 
 from __future__ import annotations
@@ -169,6 +170,70 @@ def gptq_sweep(W: torch.Tensor, U: torch.Tensor, round_col, block: int = 128) ->
     return Q
 
 
+def _ptr(t: torch.Tensor | None):
+    return t.data_ptr() if t is not None else None
+
+
+@torch.no_grad()
+def block_headers_device(W: torch.Tensor, block: int = HEX_BLOCK, col_weight: torch.Tensor | None = None):
+    """The block header on the GPU (bh_hex_block_header): (xn [n, out, in] in [-1, 1], dequant
+    scales [n, out, in / block], fp8 block codes uint8 [n, out, in / block], expert scales [n],
+    k-means weights [n, out, in] = col_weight[col] * scale^2 or None). Equal to block_headers and
+    the reference's expert_scale / block_codes on the CPU bit for bit."""
+    _lib.require_gpu(W, col_weight)
+    n, out, inp = W.shape
+    if inp % block:
+        raise ValueError(f"input width {inp} is not a multiple of the block {block}")
+    w = W.float().contiguous()
+    cw = col_weight.float().contiguous() if col_weight is not None else None
+    if cw is not None and cw.shape != (n, inp):
+        raise ValueError(f"col_weight must be [n, in] = {(n, inp)}, got {tuple(cw.shape)}")
+    xn = torch.empty_like(w)
+    scale = torch.empty(n, out, inp // block, dtype=torch.float32, device=w.device)
+    codes = torch.empty(n, out, inp // block, dtype=torch.uint8, device=w.device)
+    es = torch.empty(n, dtype=torch.float32, device=w.device)
+    wt = torch.empty_like(w) if cw is not None else None
+    lib = _lib.load()
+    _lib.check(lib.bh_hex_block_header(w.data_ptr(), n, out, inp, block, _ptr(cw), xn.data_ptr(), scale.data_ptr(),
+                                       codes.data_ptr(), _ptr(wt), es.data_ptr(), _lib.stream_of(w)),
+               "bh_hex_block_header")
+    return xn, scale, codes, es, wt
+
+
+@torch.no_grad()
+def fit_levels_device(xn: torch.Tensor, wt: torch.Tensor | None, L: int, iters: int = 20, sample: int = 1 << 17,
+                      seed: int = 0) -> torch.Tensor:
+    """fit_levels on the GPU (bh_hex_fit_levels): the same seeded sample (drawn from a CPU
+    generator), the quantile start from the sorted sample (sorting is exact) with the ranks formed
+    on the CPU as the reference's CPU run forms them, and the Lloyd rounds in the kernel. Equal to
+    fit_levels on the CPU bit for bit."""
+    _lib.require_gpu(xn, wt)
+    n, N = xn.shape
+    dev = xn.device
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    if N > sample:
+        pick = torch.randint(0, N, (sample,), generator=g).to(dev)
+        xs = xn[:, pick]
+        ws = wt[:, pick] if wt is not None else None
+    else:
+        xs, ws = xn, wt
+    xs = xs.float().contiguous()
+    ws = ws.float().contiguous() if ws is not None else torch.ones_like(xs)
+    S = xs.shape[1]
+    q = torch.linspace(0, 1, L + 2)[1:-1]                 # float32 on the CPU
+    ranks = q * (S - 1)
+    lo, hi = ranks.long(), ranks.ceil().long()
+    frac = (ranks - lo).float().contiguous().to(dev)
+    srt = xs.sort(1).values
+    q_lo = srt[:, lo.to(dev)].contiguous()
+    q_hi = srt[:, hi.to(dev)].contiguous()
+    levels = torch.empty(n, L, dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    _lib.check(lib.bh_hex_fit_levels(xs.data_ptr(), ws.data_ptr(), n, S, L, q_lo.data_ptr(), q_hi.data_ptr(),
+                                     frac.data_ptr(), iters, levels.data_ptr(), _lib.stream_of(xs)), "bh_hex_fit_levels")
+    return levels
+
+
 @torch.no_grad()
 def sweep_device(W: torch.Tensor, U: torch.Tensor, levels: torch.Tensor, block_scale: torch.Tensor,
                  scale_block: int = HEX_BLOCK, dead: torch.Tensor | None = None, block: int = 128):
@@ -211,6 +276,14 @@ def quantize_experts_gptq(W: torch.Tensor, H: torch.Tensor, L: int = 16, block: 
     if block % HEX_BLOCK:
         raise ValueError(f"the scale block must be a multiple of {HEX_BLOCK}")
     n, out, inp = W.shape
+    if W.is_cuda:
+        # header, k-means and sweep in this library's kernels; the factorisations in torch
+        cw = H.diagonal(dim1=-2, dim2=-1).float().contiguous()
+        xn, bscale, bcodes, es_w, wt = block_headers_device(W, block, cw)
+        levels = fit_levels_device(xn.reshape(n, -1), wt.reshape(n, -1), L)
+        Wd, U, dead = hessian_factor(W, H, damp)
+        Q, codes = sweep_device(Wd, U, levels, bscale, block, dead, sweep_block)
+        return {"idx": pack(codes, bits), "block_scale": bcodes, "expert_scale": es_w, "levels": levels, "q": Q}
     xn, blk, es = block_headers(W, block)
     cw = H.diagonal(dim1=-2, dim2=-1).float().view(n, 1, inp // block, block)
     wt = (cw.expand(n, out, -1, -1) * blk.pow(2)).reshape(n, -1)
@@ -222,11 +295,8 @@ def quantize_experts_gptq(W: torch.Tensor, H: torch.Tensor, L: int = 16, block: 
         return torch.gather(levels, 1, nearest_index((x / s).clamp(-1, 1), levels).reshape(n, -1)).view(x.shape) * s
 
     Wd, U, dead = hessian_factor(W, H, damp)
-    if W.is_cuda:
-        Q, codes = sweep_device(Wd, U, levels, blk[..., 0], block, dead, sweep_block)
-    else:
-        Q = gptq_sweep(Wd, U, round_col, sweep_block) * (~dead)[:, None, :]
-        codes = nearest_index((Q / scale).clamp(-1, 1), levels)
+    Q = gptq_sweep(Wd, U, round_col, sweep_block) * (~dead)[:, None, :]
+    codes = nearest_index((Q / scale).clamp(-1, 1), levels)
     es_w = (W.float().abs().amax(dim=(1, 2)) / FP8_MAX).clamp(min=1e-30)
     bs = (blk[..., 0] / es_w[:, None, None]).clamp(max=FP8_MAX).to(torch.float8_e4m3fn).view(torch.uint8)
     return {"idx": pack(codes, bits), "block_scale": bs.contiguous(), "expert_scale": es_w.float().contiguous(),

@@ -119,9 +119,161 @@ __global__ __launch_bounds__(kGqRows) void gptq_sweep_kernel(GptqArgs a) {
   }
 }
 
+// ----------------------------------------------------------------------------------- header
+
+constexpr int kHdThreads = 1024;
+constexpr float kFp8Max = 448.0f;
+
+// v in [0, 448] rounded to the nearest fp8 e4m3fn value (ties to even): a multiple of the value's
+// fp8 spacing, 2^(e - 3) for exponents e >= -6 and 2^-9 below (the subnormals). Scaling by a power
+// of two is exact, so the one rounding is the round-to-nearest-even of v / spacing.
+__device__ __forceinline__ float fp8_round(float v) {
+  const int ex = (int)((__float_as_uint(v) >> 23) & 0xFFu) - 127;
+  const int sp = (ex < -6 ? -6 : ex) - 3;
+  return __builtin_ldexpf(__builtin_rintf(__builtin_ldexpf(v, -sp)), sp);
+}
+
+// The e4m3fn code of an fp8 value q in [0, 448] (as fp8_round returns).
+__device__ __forceinline__ uint32_t fp8_code(float q) {
+  if (q == 0.0f) return 0u;
+  const uint32_t b = __float_as_uint(q);
+  const int ex = (int)((b >> 23) & 0xFFu) - 127;
+  if (ex < -6) return (uint32_t)__builtin_rintf(__builtin_ldexpf(q, 9));     // subnormal: q / 2^-9
+  return ((uint32_t)(ex + 7) << 3) | ((b >> 20) & 7u);
+}
+
+// One workgroup per expert: es = max(max|w| / 448, 1e-30); per block of `block` inputs the
+// dequant scale fp8(min(amax / es, 448)) * es (1 where that is 0), its fp8 code of
+// min(scale / es, 448), the values clamp(w / scale, -1, 1), and (col_weight given) the k-means
+// weights col_weight[col] * scale^2 (reaper/gpu_perf/headers.py:39-51, 96-98;
+// harness/blackhole_pipeline/pack.py:77-86).
+__global__ __launch_bounds__(kHdThreads) void block_header_kernel(const float* w, int64_t out, int64_t in, int block,
+                                                                  const float* col_weight, float* xn, float* scale,
+                                                                  uint8_t* codes, float* wt, float* es_out) {
+#pragma clang fp contract(off)
+  __shared__ float red[kHdThreads / kWave];
+  const int tid = threadIdx.x;
+  const int64_t e = blockIdx.x, m = out * in, nb = m / block;
+  const float* we = w + e * m;
+  float mx = 0.f;
+  for (int64_t i = tid; i < m; i += kHdThreads) mx = fmaxf(mx, fabsf(we[i]));
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  float top = 0.f;
+#pragma unroll
+  for (int i = 0; i < kHdThreads / kWave; ++i) top = fmaxf(top, red[i]);
+  const float es = fmaxf(top / kFp8Max, 1e-30f);
+  if (tid == 0) es_out[e] = es;
+  for (int64_t bk = tid; bk < nb; bk += kHdThreads) {
+    const float* x = we + bk * block;
+    float amax = 0.f;
+    for (int i = 0; i < block; ++i) amax = fmaxf(amax, fabsf(x[i]));
+    float blk = fp8_round(fminf(amax / es, kFp8Max)) * es;
+    if (!(blk > 0.0f)) blk = 1.0f;
+    scale[e * nb + bk] = blk;
+    if (codes) codes[e * nb + bk] = (uint8_t)fp8_code(fp8_round(fminf(blk / es, kFp8Max)));
+    const int64_t col0 = (bk * block) % in;
+    const float b2 = blk * blk;
+    for (int i = 0; i < block; ++i) {
+      if (xn) xn[e * m + bk * block + i] = fminf(fmaxf(x[i] / blk, -1.0f), 1.0f);
+      if (wt) wt[e * m + bk * block + i] = col_weight[e * in + col0 + i] * b2;
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------------- k-means
+
+// One wave per expert, lane l owning level l: the start is the linear-interpolation quantile
+// lo + w (hi - lo) of the sorted sample (ATen's form: an FMA on the end nearer the weight), then
+// `iters` Lloyd rounds: every value goes to the level of its left midpoint search, each level's
+// sums of x*w and w run over its values in sample order (as the CPU's scatter_add), the level
+// moves to num / max(den, 1e-30) where den > 0, and the levels are sorted
+// (reaper/gpu_perf/headers.py:66-83).
+template <int L>
+__global__ __launch_bounds__(kWave) void fit_levels_kernel(const float* xs, const float* ws, int64_t S,
+                                                           const float* q_lo, const float* q_hi, const float* q_w,
+                                                           int iters, float* levels) {
+#pragma clang fp contract(off)
+  __shared__ float srt[L];
+  const int lane = threadIdx.x;
+  const int64_t e = blockIdx.x;
+  const float* x = xs + e * S;
+  const float* wv = ws + e * S;
+  float lev = 0.f;
+  if (lane < L) {
+    const float lo = q_lo[e * L + lane], hi = q_hi[e * L + lane], wq = q_w[lane];
+    const float d = hi - lo;
+    lev = fabsf(wq) < 0.5f ? __builtin_fmaf(wq, d, lo) : __builtin_fmaf(wq - 1.0f, d, hi);
+  }
+  for (int it = 0; it < iters; ++it) {
+    float mid[L - 1];
+#pragma unroll
+    for (int mi = 0; mi < L - 1; ++mi) {
+      const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lev), mi + 1));
+      const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lev), mi));
+      mid[mi] = (a + b) / 2.0f;
+    }
+    float num = 0.f, den = 0.f;
+    for (int64_t i = 0; i < S; ++i) {
+      const float xi = x[i], wi = wv[i];
+      int a = 0;
+#pragma unroll
+      for (int mi = 0; mi < L - 1; ++mi) a += mid[mi] < xi ? 1 : 0;
+      if (a == lane) {
+        num = num + xi * wi;
+        den = den + wi;
+      }
+    }
+    if (lane < L && den > 0.0f) lev = num / fmaxf(den, 1e-30f);
+    // sort the L levels: lane l counts the levels below its own (ties by lane), then stores there
+    int rank = 0;
+#pragma unroll
+    for (int mi = 0; mi < L; ++mi) {
+      const float o = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lev), mi));
+      rank += (o < lev || (o == lev && mi < lane)) ? 1 : 0;
+    }
+    if (lane < L) srt[rank] = lev;
+    __syncthreads();
+    if (lane < L) lev = srt[lane];
+    __syncthreads();
+  }
+  if (lane < L) levels[e * L + lane] = lev;
+}
+
 }  // namespace bh
 
 using namespace bh;
+
+extern "C" int bh_hex_block_header(const float* w, int64_t n, int64_t out, int64_t in, int32_t block,
+                                   const float* col_weight, float* xn, float* scale, uint8_t* codes, float* wt,
+                                   float* expert_scale, void* stream) {
+  const char* who = "bh_hex_block_header";
+  if (n < 0 || out <= 0 || in <= 0 || block <= 0 || in % block)
+    return fail(BH_HEX_ERR_VALUE, std::string(who) + ": bad sizes (in a multiple of block)");
+  if (n == 0) return BH_HEX_OK;
+  if (!w || !scale || !expert_scale || (wt && !col_weight)) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": null pointer");
+  hipLaunchKernelGGL(block_header_kernel, dim3((unsigned)n), dim3(kHdThreads), 0, reinterpret_cast<hipStream_t>(stream),
+                     w, out, in, block, col_weight, xn, scale, codes, wt, expert_scale);
+  return check_launch(who);
+}
+
+extern "C" int bh_hex_fit_levels(const float* xs, const float* ws, int64_t n, int64_t S, int32_t n_levels,
+                                 const float* q_lo, const float* q_hi, const float* q_w, int32_t iters, float* levels,
+                                 void* stream) {
+  const char* who = "bh_hex_fit_levels";
+  if (n_levels != 8 && n_levels != 16) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": 8 or 16 levels");
+  if (n < 0 || S <= 0 || iters < 0) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": bad sizes");
+  if (n == 0) return BH_HEX_OK;
+  if (!xs || !ws || !q_lo || !q_hi || !q_w || !levels) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": null pointer");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (n_levels == 16)
+    hipLaunchKernelGGL(fit_levels_kernel<16>, dim3((unsigned)n), dim3(kWave), 0, st, xs, ws, S, q_lo, q_hi, q_w, iters, levels);
+  else
+    hipLaunchKernelGGL(fit_levels_kernel<8>, dim3((unsigned)n), dim3(kWave), 0, st, xs, ws, S, q_lo, q_hi, q_w, iters, levels);
+  return check_launch(who);
+}
 
 extern "C" int bh_hex_gptq_sweep(float* w, const float* u, const float* levels, int32_t n_levels, const float* scale,
                                  int32_t scale_block, const uint8_t* dead, int64_t n, int64_t out, int64_t in,

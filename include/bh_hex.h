@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define BH_HEX_ABI_VERSION 12
+#define BH_HEX_ABI_VERSION 13
 
 enum bh_hex_status {
   BH_HEX_OK = 0,
@@ -300,6 +300,27 @@ int bh_hex_moe_gemv(const void* x, int32_t x_dtype, int64_t s_xm, void* act, int
  * nearest to clamp(q / s, -1, 1). Every operation is the reference's on the CPU, so q and codes
  * equal its output bit for bit on the same inputs. Replaces the sweep of
  * reaper/gpu_perf/gptq.py:62-83 (_solve) and table_indices (harness/blackhole_pipeline/pack.py:53-62). */
+/* The HEX producer's block header (reaper/gpu_perf/headers.py:39-51, _blocks, non-shared scale;
+ * harness/blackhole_pipeline/pack.py:77-86, expert_scale and block_codes) for w [n, out, in]
+ * float32, in a multiple of block: expert_scale[e] = max(max|w| / 448, 1e-30); per block of
+ * `block` inputs scale = fp8(min(amax / es, 448)) * es (1 where that is 0; fp8 = e4m3fn, round to
+ * nearest even), codes (uint8, may be null) the e4m3fn code of min(scale / es, 448), xn (may be
+ * null) clamp(w / scale, -1, 1) [n, out, in], and, when col_weight [n, in] is given, the k-means
+ * weights wt [n, out, in] = col_weight[col] * scale^2 (headers.py:96-98). Divisions are IEEE, so
+ * every output equals the reference's on the CPU bit for bit. */
+int bh_hex_block_header(const float* w, int64_t n, int64_t out, int64_t in, int32_t block, const float* col_weight,
+                        float* xn, float* scale, uint8_t* codes, float* wt, float* expert_scale, void* stream);
+
+/* The weighted 1-D k-means of the HEX producer (reaper/gpu_perf/headers.py:66-83, fit_levels) for
+ * n experts of S sampled values xs [n, S] with weights ws [n, S] (the caller draws the sample as
+ * the reference does, from its CPU generator): the start is the quantile lo + w (hi - lo) of each
+ * of n_levels ranks (q_lo, q_hi [n, n_levels]: the sorted sample at the floor and ceiling of the
+ * rank; q_w [n_levels] the fractions), then `iters` Lloyd rounds (left midpoint search, each
+ * level's sums in sample order, num / max(den, 1e-30) where den > 0, sort). levels [n, n_levels].
+ * Equals the reference on the CPU bit for bit. One wave per expert. */
+int bh_hex_fit_levels(const float* xs, const float* ws, int64_t n, int64_t S, int32_t n_levels, const float* q_lo,
+                      const float* q_hi, const float* q_w, int32_t iters, float* levels, void* stream);
+
 int bh_hex_gptq_sweep(float* w, const float* u, const float* levels, int32_t n_levels, const float* scale,
                       int32_t scale_block, const uint8_t* dead, int64_t n, int64_t out, int64_t in, int32_t block,
                       float* q, uint8_t* codes, void* stream);

@@ -1,17 +1,15 @@
 """The HEX producer with GPTQ rounding on the GPU (marked gpu).
 
-The column sweep and the table indices run in the HIP kernel bh_hex_gptq_sweep. Given the
-reference's own header scales, levels and Hessian factor (computed on the CPU, where they equal
-the reference's bit for bit), its Q and packed indices equal the golden vectors the reference
-wrote, bit for bit; on multi-block shapes (lazy updates of later blocks, tail chunks, partial
-waves, 8 and 16 levels, other scale and sweep blocks, dead columns) it equals the CPU sweep bit
-for bit. The whole producer on the device (torch header, k-means and factorisations around the
-kernel): the expert scales agree to 2 ulp (torch's float32 division on the device is not
-correctly rounded), at least 99.9% of the fp8 block codes and 99% of the indices agree, the
-levels agree to float32 rounding (the k-means sums run as atomics there) and the layer error
-under the Hessian is within 1% of the reference's; on a config-2-width stack (4 experts,
-768 x 2048) GPTQ's layer error is below plain rounding's, and the parts run through the fused
-kernels."""
+The block header (bh_hex_block_header), the weighted k-means (bh_hex_fit_levels) and the column
+sweep with the table indices (bh_hex_gptq_sweep) run in HIP kernels; the damped Hessian
+factorisations are torch float64 on the device. Each kernel equals its CPU statement bit for bit:
+the header on every fp8 rounding region (subnormal scales, ties, zero blocks) and both block
+sizes, the k-means with and without the seeded sample, the sweep on multi-block shapes (lazy
+updates of later blocks, tail chunks, partial waves, 8 and 16 levels, other scale and sweep
+blocks, dead columns) and, given the reference's own header, levels and factor, on the golden
+vectors the reference wrote. The whole producer on the device equals those golden vectors bit for
+bit (scales, codes, levels, indices and Q). On a config-2-width stack (4 experts, 768 x 2048)
+GPTQ's layer error is below plain rounding's, and the parts run through the fused kernels."""
 
 from __future__ import annotations
 
@@ -49,17 +47,54 @@ def test_gptq_on_gpu_matches_reference(case):
     say(f"gptq on the GPU, case {name}")
     W, H = G.make_case(name, n, o, i, tokens, seed)
     got = gptq.quantize_experts_gptq(torch.from_numpy(W).to(DEV), torch.from_numpy(H).to(DEV), L)
-    np.testing.assert_allclose(got["expert_scale"].cpu().numpy(), GOLD[f"{name}__expert_scale"], rtol=2.5e-7, atol=0)
-    assert (got["block_scale"].cpu().numpy() == GOLD[f"{name}__block_scale"]).mean() >= 0.999
-    np.testing.assert_allclose(got["levels"].cpu().numpy(), GOLD[f"{name}__levels"], rtol=0, atol=2e-6)
-    bits = L.bit_length() - 1
-    a = O.unpack_bits(got["idx"].cpu().numpy().view(np.uint32), bits, i)
-    b = O.unpack_bits(GOLD[f"{name}__idx"].view(np.uint32), bits, i)
-    assert (a == b).mean() >= 0.99
-    Wt, Ht = torch.from_numpy(W), torch.from_numpy(H)
-    e_got = layer_err(Wt, got["q"].cpu(), Ht)
-    e_ref = layer_err(Wt, torch.from_numpy(GOLD[f"{name}__q"]), Ht)
-    assert torch.all(e_got <= e_ref * 1.01 + 1e-12), (e_got, e_ref)
+    # header, k-means, sweep and indices in the HIP kernels: every part equals the reference's
+    assert np.array_equal(got["expert_scale"].cpu().numpy(), GOLD[f"{name}__expert_scale"])
+    assert np.array_equal(got["block_scale"].cpu().numpy(), GOLD[f"{name}__block_scale"])
+    assert np.array_equal(got["levels"].cpu().numpy(), GOLD[f"{name}__levels"])
+    assert np.array_equal(got["idx"].cpu().numpy(), GOLD[f"{name}__idx"])
+    assert np.array_equal(got["q"].cpu().numpy().view(np.uint32), GOLD[f"{name}__q"].view(np.uint32))
+
+
+@pytest.mark.parametrize("block", [32, 128])
+def test_header_kernel_bit_exact(block):
+    """Expert scale, block scales, fp8 codes, normalised values and k-means weights against the CPU
+    statement (block_headers and the reference's block_codes): weights spanning the fp8 range, a
+    zero block, a block of fp8-subnormal scale and values on fp8 rounding ties."""
+    say(f"block header kernel, block {block}")
+    g = torch.Generator().manual_seed(block)
+    n, o, i = 3, 40, 512
+    W = torch.randn(n, o, i, generator=g) * torch.logspace(-6, 0, i)[None, None, :] * 0.05
+    W[0, 3, :block] = 0.0                                  # a zero block
+    W[1, 5, :block] *= 1e-4                                # an fp8-subnormal block scale
+    es = W.abs().amax(dim=(1, 2)) / 448.0
+    ties = torch.tensor([0.0029296875, 1.0625, 2.125, 17.0, 0.009765625]) * 1.0  # fp8 midpoints
+    W[2, 7, :5] = ties * es[2]
+    cw = torch.rand(n, i, generator=g) * 10
+    xn, blk, es_c = gptq.block_headers(W, block)
+    wt_c = (cw.view(n, 1, i // block, block).expand(n, o, -1, -1) * blk.pow(2)).reshape(n, o, i)
+    codes_c = (blk[..., 0] / es_c[:, None, None]).clamp(max=448).to(torch.float8_e4m3fn).view(torch.uint8)
+    xn_d, sc_d, co_d, es_d, wt_d = gptq.block_headers_device(W.to(DEV), block, cw.to(DEV))
+    assert torch.equal(es_d.cpu(), es_c)
+    assert torch.equal(sc_d.cpu(), blk[..., 0])
+    assert torch.equal(co_d.cpu(), codes_c)
+    assert torch.equal(xn_d.cpu(), xn.reshape(n, o, i))
+    assert torch.equal(wt_d.cpu(), wt_c)
+
+
+@pytest.mark.parametrize("L,N", [(16, 5000), (8, 3000), (16, 200_000)])
+def test_fit_levels_kernel_bit_exact(L, N):
+    """The weighted k-means against fit_levels on the CPU: with all values, and above 2^17 values
+    through the seeded sample."""
+    say(f"k-means kernel L={L} N={N}")
+    g = torch.Generator().manual_seed(L + N)
+    n = 3
+    xn = (torch.randn(n, N, generator=g) * 0.4).clamp(-1, 1)
+    wt = torch.rand(n, N, generator=g) * 3
+    wt[1, : N // 3] = 0.0
+    want = gptq.fit_levels(xn, wt, L)
+    got = gptq.fit_levels_device(xn.to(DEV), wt.to(DEV), L)
+    assert torch.equal(got.cpu(), want)
+    assert torch.equal(gptq.fit_levels_device(xn.to(DEV), None, L).cpu(), gptq.fit_levels(xn, None, L))
 
 
 def _cpu_inputs(W, H, L, block=32):
