@@ -188,6 +188,7 @@ def kernel_breakdown(cfg, copies, x, w, ids, reps):
             for tiers in copies:
                 hm.hex_moe_gemv(x, w, ids, tiers[0])
         return {"gemv_us": event_time_ms(graph_of(gemv), reps) * 1e3 / len(copies),
+                "kernel": "gemv_glu_kernel + gemv_down_kernel (the whole layer)",
                 "tiles": {"path": "matrix-vector: bh_hex_moe_gemv (gate/up, then down with the k-slot sum)"}}
     flat = ids.reshape(-1)
     ids_flat, code = hm._ids_arg(flat)
@@ -465,7 +466,7 @@ def rocprof_summary(dirs: list[str]) -> str:
                 agg.setdefault(key, []).append(float(r["Counter_Value"]))
             out.append(f"## counters, mean per dispatch ({d})")
             for (k, c), v in sorted(agg.items()):
-                if any(s in k for s in ("hex_moe", "hex_gemm", "align_", "moe_reduce", "bitwise_not")):
+                if any(s in k for s in ("hex_moe", "hex_gemm", "gemv_", "align_", "moe_reduce", "bitwise_not")):
                     out.append(f"{k:<112} {c:<12} {sum(v) / len(v):>14.1f}  (n={len(v)})")
                 counters.setdefault(c, {})[k] = v
     if "SQ_VALU_MFMA_BUSY_CYCLES" in counters and "GRBM_GUI_ACTIVE" in counters:
@@ -563,7 +564,7 @@ def main(argv=None) -> int:
         gbs = head["layer_bytes"] / (k["gemv_us"] * 1e-6) / 1e9
         roofline = {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": gbs / HBM_PEAK_GBS, "traffic": None, "traffic_source": None,
-                    "kernel": "gemv_glu_kernel + gemv_down_kernel (the whole layer)",
+                    "kernel": k["kernel"],
                     "algorithmic_bytes_per_launch": head["layer_bytes"], "avg_launch_us": k["gemv_us"]}
 
     sweep = {}
