@@ -16,6 +16,7 @@ namespace bh {
 template <int BITS, int ADT, bool GLU, int MT, int SB, bool KF>
 __global__ __launch_bounds__(kThreads) void hex_moe_kernel(MoeArgs a) {
   __shared__ MoeSmem<BITS, GLU, MT> sm;
+  touch_args<MoeArgs>();
   moe_range<BITS, ADT, GLU, MT, SB, KF>(a, sm, blockIdx.x, threadIdx.x);
 }
 

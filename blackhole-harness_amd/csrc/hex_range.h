@@ -72,7 +72,8 @@ constexpr int kMinUnits = 2;             // units per workgroup below which the 
 
 // Units per trip P: the weight loads of P units are in flight per wave ahead of the math, and
 // the activation tiles of the next P units are fetched one trip ahead; one workgroup barrier
-// per trip publishes them.
+// per trip publishes them. (Four units per trip for the 16-slot down kernel measured slower at
+// config 2, T=16: 66.9 against 64.6 us per layer; its larger first trip delays the prologue.)
 template <int MT, bool GLU>
 constexpr int trip() { return GLU ? (MT == 1 ? 2 : 1) : (MT == 4 ? 1 : 2); }
 
