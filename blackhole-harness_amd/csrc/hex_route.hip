@@ -207,14 +207,17 @@ __global__ __launch_bounds__(kAlignThreads) void align_count_kernel(const void* 
                                                                     int32_t n, const int32_t* __restrict__ lookup,
                                                                     int32_t* __restrict__ ws) {
   __shared__ int cnt[kAlignMaxExperts];
+  __shared__ int lk[TIER ? kAlignMaxExperts : 1];   // the tier lookup
   const int tid = threadIdx.x;
-  for (int e = tid; e < n; e += kAlignThreads) cnt[e] = 0;
-  __syncthreads();
+  // the slot's id and the lookup together (one round trip; the lookup of the id then from LDS)
   const int64_t i = (int64_t)blockIdx.x * kAlignThreads + tid;
-  if (i < S) {
-    const int64_t e = placed_id<IDT, TIER>(ids, i, n, lookup);
-    if (e >= 0) atomicAdd(&cnt[e], 1);
+  const int64_t id = i < S ? load_id<IDT>(ids, i) : -1;
+  for (int e = tid; e < n; e += kAlignThreads) {
+    cnt[e] = 0;
+    if constexpr (TIER) lk[e] = lookup[e];
   }
+  __syncthreads();
+  if (id >= 0 && id < n && (!TIER || lk[TIER ? id : 0] >= 0)) atomicAdd(&cnt[id], 1);
   __syncthreads();
   for (int e = tid; e < n; e += kAlignThreads) ws[(int64_t)blockIdx.x * n + e] = cnt[e];
 }
@@ -285,6 +288,94 @@ __global__ __launch_bounds__(kAlignThreads) void align_scatter_kernel(const void
   }
 }
 
+// The block plan and the placement in one launch after align_count_kernel, one workgroup per
+// 1024-slot chunk, when every chunk's counts fit in LDS (chunks x experts <= kPlaceMaxCounts).
+// Each workgroup reads all chunks' counts, forms each expert's total and its slots in earlier
+// chunks, scans the experts' block counts for their runs' first rows, and places its own slots
+// as align_scatter_kernel does. The block plan's other rows are spread over the workgroups:
+// expert e's blocks and unfilled rows by workgroup e % chunks, the rows and blocks past the used
+// ones in turn. Same result as align_kernel<IDT, false> followed by align_scatter_kernel.
+constexpr int kPlaceMaxCounts = kAlignWaves * kAlignMaxExperts;
+
+template <int IDT, bool TIER>
+__global__ __launch_bounds__(kAlignThreads) void align_place_kernel(const void* __restrict__ ids, int64_t S,
+                                                                    int32_t n, const int32_t* __restrict__ lookup,
+                                                                    int32_t bm, int64_t max_blocks,
+                                                                    int32_t* __restrict__ sorted_ids,
+                                                                    int32_t* __restrict__ expert_ids,
+                                                                    int32_t* __restrict__ npp,
+                                                                    const int32_t* __restrict__ ws) {
+  __shared__ int lc[kPlaceMaxCounts];        // every chunk's counts, [chunk][expert]
+  __shared__ int wcnt[kAlignWaves][kAlignMaxExperts];   // per wave: count, then offset in the run
+  __shared__ int pre[kAlignMaxExperts];      // the expert's slots in earlier chunks
+  __shared__ int start[kAlignMaxExperts];    // first padded row of the expert's run
+  __shared__ int wsum[kAlignWaves];
+  __shared__ int total_blocks;
+  __shared__ int lk[TIER ? kAlignMaxExperts : 1];   // the tier lookup
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int nch = (int)gridDim.x, c = (int)blockIdx.x;
+  int nbits = 1;
+  while ((1 << nbits) <= n) ++nbits;
+  const uint64_t below = (lane ? (~0ull >> (64 - lane)) : 0ull);
+  // every chunk's counts (all loads before any store: indices past the last repeat it, so no
+  // branch and no wait between them), then this thread's slot
+  const int nv = nch * n;
+  constexpr int kPT = kPlaceMaxCounts / kAlignThreads;
+  int cv[kPT];
+#pragma unroll
+  for (int q = 0; q < kPT; ++q) cv[q] = ws[min(tid + q * kAlignThreads, nv - 1)];
+  const int64_t i = (int64_t)c * kAlignThreads + tid;
+  const int64_t id = i < S ? load_id<IDT>(ids, i) : -1;
+  if constexpr (TIER)
+    for (int e = tid; e < n; e += kAlignThreads) lk[e] = lookup[e];
+  for (int e = lane; e < n; e += kWave) wcnt[w][e] = 0;
+#pragma unroll
+  for (int q = 0; q < kPT; ++q)
+    if (tid + q * kAlignThreads < nv) lc[tid + q * kAlignThreads] = cv[q];
+  __syncthreads();
+  const int key = (id >= 0 && id < n && (!TIER || lk[TIER ? id : 0] >= 0)) ? (int)id : n;
+  // thread e: expert e's slots in earlier chunks and in all (n <= kAlignThreads)
+  int tot = 0;
+  if (tid < n) {
+    for (int cc = 0; cc < nch; ++cc) {
+      if (cc == c) pre[tid] = tot;
+      tot += lc[cc * n + tid];
+    }
+  }
+  const int nb = (tot + bm - 1) / bm;
+  const int incl = block_incl_scan(nb, wsum);  // (its barriers order the LDS accesses around it)
+  const int run = incl - nb;                   // blocks before expert tid's run
+  if (tid < n) start[tid] = run * bm;
+  if (tid == kAlignThreads - 1) total_blocks = incl;
+  const uint64_t same = match_key(key, nbits);
+  const int rank = __popcll(same & below);
+  if (key < n && rank == 0) wcnt[w][key] = __popcll(same);
+  __syncthreads();
+  const int used = total_blocks;
+  if (tid < n && tid % nch == c) {
+    for (int b = run; b < run + nb; ++b) expert_ids[b] = tid;
+    for (int64_t r = (int64_t)run * bm + tot; r < (int64_t)(run + nb) * bm; ++r) sorted_ids[r] = (int32_t)S;
+  }
+  const int64_t step = (int64_t)nch * kAlignThreads;
+  for (int64_t b = used + (int64_t)c * kAlignThreads + tid; b < max_blocks; b += step) expert_ids[b] = -1;
+  for (int64_t r = (int64_t)used * bm + (int64_t)c * kAlignThreads + tid; r < max_blocks * bm; r += step)
+    sorted_ids[r] = (int32_t)S;
+  if (c == 0 && tid == 0) npp[0] = used * bm;
+  for (int e = tid; e < n; e += kAlignThreads) {        // offsets: earlier chunks, then earlier waves
+    int acc = pre[e];
+    for (int v = 0; v < kAlignWaves; ++v) {
+      const int cw = wcnt[v][e];
+      wcnt[v][e] = acc;
+      acc += cw;
+    }
+  }
+  __syncthreads();
+  if (key < n) {
+    const int64_t pos = (int64_t)start[key] + wcnt[w][key] + rank;
+    if (pos < max_blocks * bm) sorted_ids[pos] = (int32_t)i;
+  }
+}
+
 template <int IDT>
 __global__ __launch_bounds__(256) void direct_kernel(const void* __restrict__ ids, int64_t S, int32_t bm,
                                                      int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids,
@@ -328,19 +419,26 @@ static int align_run(const char* who, const void* ids, int32_t ids_dtype, int64_
   const int64_t max_blocks = bh_hex_align_max_blocks(S, n_experts, block_m);
   if (max_blocks * block_m > (int64_t)INT32_MAX) return fail(BH_HEX_ERR_VALUE, w + ": plan too large");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  // up to kAlignSplit slots one workgroup does everything; above, it writes the block plan and
-  // one workgroup per 1024 slots places them (with a workspace, one workgroup per 1024 slots
-  // first counts them, so that no workgroup counts more than its own chunk)
+  // up to kAlignSplit slots one workgroup does everything; above, with a workspace, one workgroup
+  // per 1024 slots first counts them, and then (when every chunk's counts fit in LDS) one
+  // workgroup per chunk forms the block plan and places its slots; otherwise one workgroup writes
+  // the block plan and one per chunk places the slots
   const bool split = S > kAlignSplit;
   if (!split) ws = nullptr;
   if (ws && ws_len < bh_hex_align_workspace(S, n_experts)) return fail(BH_HEX_ERR_VALUE, w + ": workspace too small");
   const dim3 chunks((unsigned)cdiv(S, kAlignThreads));
   const dim3 one(1), threads(kAlignThreads);
+  const bool place = ws && cdiv(S, kAlignThreads) * n_experts <= kPlaceMaxCounts;
 #define BH_ALIGN(IDT, TIER)                                                                                       \
   do {                                                                                                            \
     if (split) {                                                                                                  \
       if (ws)                                                                                                     \
         hipLaunchKernelGGL((align_count_kernel<IDT, TIER>), chunks, threads, 0, st, ids, S, n_experts, lookup, ws); \
+      if (place) {                                                                                                \
+        hipLaunchKernelGGL((align_place_kernel<IDT, TIER>), chunks, threads, 0, st, ids, S, n_experts, lookup,    \
+                           block_m, max_blocks, sorted_ids, expert_ids, npp, ws);                                 \
+        break;                                                                                                    \
+      }                                                                                                           \
       hipLaunchKernelGGL((align_kernel<IDT, false, TIER>), one, threads, 0, st, ids, S, n_experts, lookup,        \
                          block_m, max_blocks, sorted_ids, expert_ids, npp, ws);                                   \
       hipLaunchKernelGGL((align_scatter_kernel<IDT, TIER>), chunks, threads, 0, st, ids, S, n_experts, lookup,    \
