@@ -441,6 +441,35 @@ def layer_sequence(trace: list) -> list[str]:
     return out
 
 
+def prefill_timeline(trace: list, last: int = 1) -> list[str]:
+    """Every dispatch of the last `last` replayed prefill layers (the dispatches between two
+    k-slot sums that include both prefill kernels), with queue, start and end in microseconds from
+    the end of the previous layer's sum."""
+    def role(n: str) -> str:
+        for key, r in (("align_count", "count"), ("align_place", "place"), ("align_scatter", "scatter"),
+                       ("align_kernel", "plan"), ("moe_reduce", "sum")):
+            if key in n:
+                return r
+        if PREFILL_GLU_KERNEL.split("<")[0] in n:
+            return "gate/up" if n.split("<", 1)[1].split(",")[2].strip() == "true" else "down"
+        return ""
+    rows = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), role(r["Kernel_Name"]), r.get("Queue_Id", ""))
+                  for r in trace)
+    rows = [r for r in rows if r[2]]
+    sums = [i for i, r in enumerate(rows) if r[2] == "sum"]
+    layers = [(a, b) for a, b in zip(sums, sums[1:])
+              if {"gate/up", "down"} <= {r[2] for r in rows[a + 1:b]} and b - a < 40]
+    out = []
+    for a, b in layers[-last:]:
+        t0 = rows[a][1]
+        out.append(f"## prefill layer timeline ({b - a} dispatches, span {(rows[b][1] - t0) / 1e3:.1f} us after "
+                   f"the previous sum)")
+        for s0, e0, r, q in rows[a + 1:b + 1]:
+            out.append(f"   {r:8s} q={q:>3s} start {(s0 - t0) / 1e3:8.1f} end {(e0 - t0) / 1e3:8.1f} "
+                       f"dur {(e0 - s0) / 1e3:7.1f}")
+    return out
+
+
 def rocprof_summary(dirs: list[str]) -> str:
     """Text summary of rocprofv3 CSV output directories: per-kernel dispatch statistics from a
     --kernel-trace --stats run, mean counter values per dispatch from --pmc runs, and, when a
@@ -449,7 +478,9 @@ def rocprof_summary(dirs: list[str]) -> str:
     (written to TRAFFIC_FILE)."""
     out, counters = [], {}
     for d in dirs:
-        out += layer_sequence(list(_csv_rows(d, "kernel_trace.csv")))
+        trace = list(_csv_rows(d, "kernel_trace.csv"))
+        out += layer_sequence(trace)
+        out += prefill_timeline(trace)
         stats = list(_csv_rows(d, "kernel_stats.csv"))
         if stats:
             out.append(f"## kernel statistics ({d})")
