@@ -182,7 +182,7 @@ def kernel_breakdown(cfg, copies, x, w, ids, reps):
     T, k = ids.shape
     S = T * k
     E, H, I = cfg["E"], cfg["H"], cfg["I"]
-    if len(copies[0]) == 1 and 0 < S <= hm.GEMV_MAX and hm.gemv_fits(k, H, I):
+    if len(copies[0]) == 1 and hm.gemv_prefer(T, k, H, I, copies[0][0]):
         # hex_moe_fused runs the layer as the two matrix-vector launches of one call
         def gemv():
             for tiers in copies:

@@ -51,12 +51,18 @@ SPLIT = int(os.environ.get("BLACKHOLE_HEX_SPLIT", "2"))
 # slots up to which the decode kernels sort the slots by expert themselves (bh_hex_moe_*_ids), so
 # no align launch precedes them (at most 1024; 0 always launches the align kernel)
 KERNEL_PLAN_MAX = min(1024, int(os.environ.get("BLACKHOLE_HEX_KERNEL_PLAN_MAX", "1024")))
-# slots up to which a single tier's layer runs as two matrix-vector launches (bh_hex_moe_gemv:
-# no plan, no workspace, the k-slot sum inside the down launch); 0 never. Measured against the
-# expert-block kernels (layer us, top-8): config 2 widths T=1 13.6 vs 38.8, T=4 26.5 vs 48.4,
-# T=8 44.0 vs 60.2, T=12 68.0 vs 58.2; hidden 4096 / 1536 wide experts T=4 76.6 vs 92.6, T=6 110.9
-# vs 104.6. The gap closes as slots share experts (each slot reads its expert's weights).
-GEMV_MAX = int(os.environ.get("BLACKHOLE_HEX_GEMV_MAX", "32"))
+# A single tier's layer runs as two matrix-vector launches (bh_hex_moe_gemv: no plan, no
+# workspace, the k-slot sum inside the down launch) at up to GEMV_MAX slots (0: never) while the
+# weight bytes that slots sharing an expert read again stay within GEMV_EXTRA_MB: (slots -
+# expected distinct experts) x one expert's bytes, with E (1 - (1 - k/E)^T) distinct experts
+# under uniform routing. The matrix-vector launches read each slot's expert once per slot; the
+# expert-block kernels read each routed expert once but pay a plan, a workspace exchange and a
+# third launch. Measured (layer us, matrix-vector vs expert-block, top-8): 96 experts of 2048 x
+# 768: T=6 34.6 vs 52.3, T=8 41.3 vs 57.3 (38 MB read again), T=10 50.9 vs 54.7 (58 MB), T=12 64.7
+# vs 55.8 (81 MB); 128 experts of 4096 x 1536: T=4 72.2 vs 89.8 (28 MB), T=5 88.5 vs 92.0 (45 MB),
+# T=6 105.7 vs 101.8 (66 MB).
+GEMV_MAX = int(os.environ.get("BLACKHOLE_HEX_GEMV_MAX", "256"))
+GEMV_EXTRA_MB = float(os.environ.get("BLACKHOLE_HEX_GEMV_EXTRA_MB", "62"))
 
 
 def _n_in(p: dict, bits: int) -> int:
@@ -90,6 +96,7 @@ class HexTier:
     # the tier's SPLIT parts by expert (views of the same tensors), for hex_moe_fused's streams
     _parts: list | None = field(default=None, repr=False, compare=False)
     _is_part: bool = field(default=False, repr=False, compare=False)
+    _expert_bytes: int = field(default=0, repr=False, compare=False)   # one expert's parts, all projections
 
     def prepare(self, num_experts: int) -> "HexTier":
         """Kernel-ready views (uint32 words as int32, float32 scales and levels, contiguous) and
@@ -120,6 +127,8 @@ class HexTier:
         self.experts = self.experts.to(dev).to(torch.int32)
         self._structs = {name: _proj_struct(getattr(self, name), self.bits) for name in PROJS}
         n = len(self.experts)
+        self._expert_bytes = sum(int(p["idx"][0].numel()) * 4 + int(p["block_scale"][0].numel()) * 1 + 4
+                                 + int(p["levels"][0].numel()) * 4 for p in (getattr(self, q) for q in PROJS)) if n else 0
         if not self._is_part and SPLIT > 1 and n >= SPLIT:
             self._parts = [self._part(n * j // SPLIT, n * (j + 1) // SPLIT, num_experts) for j in range(SPLIT)]
         return self
@@ -391,6 +400,17 @@ def gemv_fits(k: int, H: int, I: int) -> bool:
     return 0 < k <= 16 and H % HEX_BLOCK == 0 and I % HEX_BLOCK == 0 and H <= 4096 and I <= 2048
 
 
+def gemv_prefer(T: int, k: int, H: int, I: int, tier: HexTier) -> bool:
+    """Whether hex_moe_fused runs a single tier's layer of T tokens as the matrix-vector
+    launches (see GEMV_MAX and GEMV_EXTRA_MB)."""
+    S = T * k
+    if not (0 < S <= GEMV_MAX and gemv_fits(k, H, I)):
+        return False
+    E = max(1, tier.lookup.numel())
+    distinct = E * (1.0 - (1.0 - min(1.0, k / E)) ** T)
+    return (S - distinct) * tier._expert_bytes <= GEMV_EXTRA_MB * 1e6
+
+
 def hex_moe_gemv(x, topk_weights, topk_ids, tier: HexTier) -> torch.Tensor:
     """Routed-expert output [T, H] in x.dtype of one tier for a few tokens, as two matrix-vector
     launches (bh_hex_moe_gemv): gate/up for every slot, then down with the top-k weights and the
@@ -447,8 +467,7 @@ def hex_moe_fused(x, topk_weights, topk_ids, tiers: list[HexTier], config: dict 
     H = x.shape[1]
     I = tiers[0].gate_proj["idx"].shape[1]
     E = tiers[0].lookup.numel()
-    if (len(tiers) == 1 and config is None and align_mode == "auto" and 0 < S <= GEMV_MAX
-            and gemv_fits(k, H, I)):
+    if len(tiers) == 1 and config is None and align_mode == "auto" and gemv_prefer(T, k, H, I, tiers[0]):
         return hex_moe_gemv(x, topk_weights, topk_ids, tiers[0])
     x = x.contiguous()
     out = torch.empty(T, H, dtype=x.dtype, device=x.device)

@@ -100,7 +100,7 @@ def test_full_shape_layer(name, E, H, I, k, groups, T, zipf, monkeypatch):
         # is set (the fused results do not depend on timing, so they are equal bit for bit)
         assert torch.equal(hm.hex_moe(x, w, ids, tiers), fused)
     blocks = fused
-    if len(tiers) == 1 and T * k <= hm.GEMV_MAX and hm.gemv_fits(k, H, I):
+    if len(tiers) == 1 and hm.gemv_prefer(T, k, H, I, tiers[0]):
         # the layer ran as the two matrix-vector launches; now through the expert-block kernels
         monkeypatch.setattr(hm, "GEMV_MAX", 0)
         blocks = hm.hex_moe_fused(x, w, ids, tiers)

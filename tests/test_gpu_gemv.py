@@ -78,7 +78,7 @@ def test_gemv_config2_widths(T, bits, block, dt):
     blocks = hm.hex_moe_fused(xd, wd, idd, [tier], {"BLOCK_M": 16}).float().cpu().numpy()
     assert O.rel_err(g, blocks) < 4e-3
     # the dispatcher takes this path for a single tier at these batches
-    if T * k <= hm.GEMV_MAX:
+    if hm.gemv_prefer(T, k, H, I, tier):
         assert torch.equal(hm.hex_moe_fused(xd, wd, idd, [tier]), got)
 
 

@@ -519,6 +519,7 @@ def test_capture_records_no_fill(monkeypatch):
     come from the zeroed arena, so the capture calls no torch.zeros (no fill kernel replays with
     the layer), and every replay equals the eager result."""
     say("capture records no fill")
+    monkeypatch.setattr(hm, "GEMV_MAX", 0)   # the expert-block kernels, whose workspace this is about
     E, H, I, k, T = 16, 512, 256, 4, 24
     ref, tiers = make_layer(E, H, I, 0, (4,), seed=60, block=128)
     w, ids = routing(T, E, k, seed=60)
@@ -535,11 +536,9 @@ def test_capture_records_no_fill(monkeypatch):
     s = torch.cuda.Stream()
     assert _ws_key(s) not in hm._WORKSPACES
     with torch.cuda.graph(g, stream=s):
-        monkeypatch.setattr(torch, "zeros", no_zeros)
-        try:
+        with monkeypatch.context() as m:
+            m.setattr(torch, "zeros", no_zeros)
             out = hm.hex_moe_fused(x, wd, idd, tiers)
-        finally:
-            monkeypatch.undo()
     assert _ws_key(s) in hm._WORKSPACES
     for i in range(3):
         g.replay()
@@ -549,7 +548,7 @@ def test_capture_records_no_fill(monkeypatch):
         torch.cuda.synchronize()
 
 
-def test_workspace_kept_alive_when_it_grows():
+def test_workspace_kept_alive_when_it_grows(monkeypatch):
     """Warm-up and capture on one stream, then an eager call on that stream whose workspace must
     grow: the graph's buffers stay allocated (nothing else is given their memory), and replays
     still equal the eager result."""
@@ -563,7 +562,8 @@ def test_workspace_kept_alive_when_it_grows():
         w, ids = routing(T, E, k, seed=seed)
         x = torch.randn(T, H, generator=torch.Generator().manual_seed(seed)).to(torch.bfloat16).to(DEV)
         return x, torch.from_numpy(w).to(DEV), torch.from_numpy(ids).to(DEV)
-    xs, ws_, ids_s = inputs(hm.GEMV_MAX // k + 1, 61)   # past the matrix-vector path: a small workspace
+    monkeypatch.setattr(hm, "GEMV_MAX", 0)   # the expert-block kernels (their workspaces) at every batch
+    xs, ws_, ids_s = inputs(5, 61)          # 20 slots: a small workspace
     xb, wb, idb = inputs(64, 62)            # 256 slots on 32-slot blocks: a larger one
     with torch.cuda.stream(s):
         eager = hm.hex_moe_fused(xs, ws_, ids_s, tiers)

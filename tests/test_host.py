@@ -92,6 +92,29 @@ def test_default_config_and_env(monkeypatch):
     assert hm._fit_tile(32, 160, 99, True) == 32
 
 
+def _zero_tier(n_local, E, H, I, bits=4, block=128):
+    def proj(o, i):
+        return {"idx": torch.zeros(n_local, o, i // 32 * bits, dtype=torch.int32),
+                "block_scale": torch.zeros(n_local, o, i // block, dtype=torch.uint8),
+                "expert_scale": torch.ones(n_local), "levels": torch.zeros(n_local, 1 << bits)}
+    return hm.HexTier(bits, torch.arange(n_local, dtype=torch.int32), proj(I, H), proj(I, H), proj(H, I)).prepare(E)
+
+
+def test_gemv_prefer_follows_the_measured_crossovers(monkeypatch):
+    """The matrix-vector launches are taken while the bytes that slots sharing an expert read again
+    stay within GEMV_EXTRA_MB: at 96 experts of 2048 x 768 (top-8) up to 10 tokens (measured
+    faster at 8 and 10, slower at 12), at 128 experts of 4096 x 1536 up to 5 (faster at 4 and 5,
+    slower at 6); never past GEMV_MAX slots or the launches' width limits."""
+    t2 = _zero_tier(2, 96, 2048, 768)
+    assert t2._expert_bytes == 3 * 768 * 2048 // 2 + 2 * 768 * 16 + 2048 * 6 + 3 * (4 + 16 * 4)
+    assert [T for T in range(1, 17) if hm.gemv_prefer(T, 8, 2048, 768, t2)] == list(range(1, 11))
+    t5 = _zero_tier(2, 128, 4096, 1536)
+    assert [T for T in range(1, 17) if hm.gemv_prefer(T, 8, 4096, 1536, t5)] == list(range(1, 6))
+    assert not hm.gemv_prefer(0, 8, 2048, 768, t2) and not hm.gemv_prefer(1, 17, 2048, 768, t2)
+    monkeypatch.setattr(hm, "GEMV_MAX", 0)
+    assert not hm.gemv_prefer(1, 8, 2048, 768, t2)
+
+
 def test_kernels_refuse_cpu_tensors():
     x = torch.zeros(2, 64, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="GPU"):
