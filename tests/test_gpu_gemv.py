@@ -62,7 +62,7 @@ def act_name(dt):
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("bits,block", [(4, 128), (3, 128), (4, 32)])
-@pytest.mark.parametrize("T", [1, 2, 4])
+@pytest.mark.parametrize("T", [1, 2, 4, 8, 10])
 def test_gemv_config2_widths(T, bits, block, dt):
     """96 experts, hidden 2048, intermediate 768, top-8 (the decode configurations' layer)."""
     say(f"gemv T={T} bits={bits} block={block} {dt}")
