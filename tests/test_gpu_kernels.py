@@ -367,6 +367,33 @@ def test_down_kernel_exact(bits):
         assert torch.equal(y16.cpu(), torch.from_numpy(want.astype(np.float32)).to(torch.bfloat16)), bm
 
 
+@pytest.mark.parametrize("T", [3, 9, 24])
+def test_repeated_experts_within_a_token(T, monkeypatch):
+    """Routing ids that repeat an expert within a token (the reference's align takes any ids): one
+    expert can then hold more slots than tokens (up to T * k), so its run spans several 16-slot
+    blocks. Through the matrix-vector launches and through the expert-block kernels (both plans),
+    against the oracle, which sums every slot."""
+    say(f"repeated experts T={T}")
+    E, H, I, k = 8, 256, 128, 4
+    ref, tiers = make_layer(E, H, I, 0, (4,), seed=31)
+    rng = np.random.default_rng(T)
+    ids = np.where(rng.random((T, k)) < 0.6, 2, rng.integers(0, E, (T, k))).astype(np.int64)
+    ids[:, 0] = 5                                    # expert 5 once per token, expert 2 often repeated
+    w = rng.random((T, k)).astype(np.float32)
+    x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to(torch.bfloat16)
+    want = O.moe_reference(x.float().numpy(), w, ids, ref, "bf16")
+    xd, wd, idd = x.to(DEV), torch.from_numpy(w).to(DEV), torch.from_numpy(ids).to(DEV)
+    assert T < 24 or (ids == 2).sum() > 32            # (T = 24: expert 2 spans three blocks)
+    gemv = hm.hex_moe_gemv(xd, wd, idd, tiers[0])
+    assert O.rel_err(gemv.float().cpu().numpy(), want) < TOL_16
+    monkeypatch.setattr(hm, "GEMV_MAX", 0)
+    for mode in ("auto", "vllm"):
+        got = hm.hex_moe_fused(xd, wd, idd, tiers, {"BLOCK_M": 16}, mode)
+        assert O.rel_err(got.float().cpu().numpy(), want) < TOL_16, mode
+    got = hm.hex_moe_fused(xd, wd, idd, tiers)
+    assert O.rel_err(got.float().cpu().numpy(), want) < TOL_16
+
+
 def test_uncovered_experts_contribute_nothing():
     say("uncovered experts")
     E, H, I, k = 8, 64, 32, 2
