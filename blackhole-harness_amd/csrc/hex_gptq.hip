@@ -9,7 +9,9 @@
 // Each weight row's sweep depends only on that row and the factor U, so one lane owns one row.
 // The row's current block lives in LDS column-major (lane r's value of column c at [c][r]: lanes
 // never share a bank), and the block's errors replace its columns as they are finalised. The
-// factor's values are the same for every lane and come in through scalar loads. The arithmetic
+// factor's values are the same for every lane: the block's diagonal part is staged in LDS once
+// per block, and the later columns' part goes through LDS 16 columns at a time, the next chunk
+// (with the rows' weights it updates) requested while the current one is applied. The arithmetic
 // is the reference's on the CPU, operation for operation: IEEE divides, a product and a
 // difference rounded separately in the block update (no contraction), and the later columns'
 // update as one fused multiply-add chain over the block's errors in column order, which is how
@@ -24,6 +26,8 @@ namespace bh {
 constexpr int kGqRows = kWave;          // rows of a workgroup: one per lane
 constexpr int kGqBlock = 128;           // most columns of one sweep block (the LDS block)
 constexpr int kGqChunk = 16;            // later columns updated together
+constexpr int kGqChunkLoads = kGqBlock * kGqChunk / kGqRows;   // factor values per lane per chunk
+constexpr int kGqScales = kGqBlock / 32 + 1;                    // a block's scale blocks (at least 32 inputs)
 
 struct GptqArgs {
   float* w;                 // [n, out, in] working weights (the sweep updates them)
@@ -50,10 +54,17 @@ __device__ __forceinline__ float level_at(int i, float levv) {
   return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(i * 4, __builtin_bit_cast(int, levv)));
 }
 
+struct GqLds {
+  float lw[kGqBlock][kGqRows];              // the rows' current block, column-major
+  float ub[kGqBlock][kGqBlock];             // U[b0 + k][b0 + c] of the block
+  float uc[2][kGqBlock][kGqChunk];          // U[b0 + k][c0 + i] of a later chunk, two chunks
+  float ls[kGqScales][kGqRows];             // the rows' scales of the block's scale blocks
+};
+
 template <int L>
 __global__ __launch_bounds__(kGqRows) void gptq_sweep_kernel(GptqArgs a) {
 #pragma clang fp contract(off)
-  __shared__ float lw[kGqBlock][kGqRows];
+  __shared__ GqLds sm;
   const int lane = threadIdx.x;
   const int e = blockIdx.y;
   const int r = blockIdx.x * kGqRows + lane;
@@ -68,54 +79,124 @@ __global__ __launch_bounds__(kGqRows) void gptq_sweep_kernel(GptqArgs a) {
   float mid[L - 1];                     // the midpoints, as the reference forms them: (a + b) / 2
 #pragma unroll
   for (int m = 0; m < L - 1; ++m) mid[m] = (le[m + 1] + le[m]) / 2.0f;
+  // factor values of one later chunk for this lane: entry t is U[b0 + k][c0 + i] with
+  // (k, i) = ((lane + 64 t) / 16, (lane + 64 t) % 16); nothing past the block or the matrix
+  auto chunk_load = [&](float (&v)[kGqChunkLoads], int b0, int cols, int c0) {
+#pragma unroll
+    for (int t = 0; t < kGqChunkLoads; ++t) {
+      const int x = lane + kGqRows * t, k = x / kGqChunk, i = x % kGqChunk;
+      v[t] = (k < cols && c0 + i < a.in) ? ue[(int64_t)(b0 + k) * in + c0 + i] : 0.f;
+    }
+  };
+  auto chunk_store = [&](const float (&v)[kGqChunkLoads], int buf) {
+#pragma unroll
+    for (int t = 0; t < kGqChunkLoads; ++t) {
+      const int x = lane + kGqRows * t;
+      sm.uc[buf][x / kGqChunk][x % kGqChunk] = v[t];
+    }
+  };
+  // the row's weights of a later chunk
+  auto row_load = [&](float (&v)[kGqChunk], int c0) {
+#pragma unroll
+    for (int i = 0; i < kGqChunk; ++i) v[i] = (row && c0 + i < a.in) ? wr[c0 + i] : 0.f;
+  };
   for (int b0 = 0; b0 < a.in; b0 += a.block) {
     const int cols = min(a.block, a.in - b0);
-    for (int c = 0; c < cols; ++c) lw[c][lane] = row ? wr[b0 + c] : 0.f;
+    // the block: the rows' weights, the factor's diagonal part and the rows' scales, all
+    // requested before any is stored
+    for (int c = 0; c < cols; c += kGqChunk) {
+      float v[kGqChunk];
+#pragma unroll
+      for (int i = 0; i < kGqChunk; ++i) v[i] = (row && c + i < cols) ? wr[b0 + c + i] : 0.f;
+#pragma unroll
+      for (int i = 0; i < kGqChunk; ++i)
+        if (c + i < cols) sm.lw[c + i][lane] = v[i];
+    }
+    for (int x0 = 0; x0 < cols * cols; x0 += kGqRows * kGqChunk) {
+      float v[kGqChunk];
+#pragma unroll
+      for (int t = 0; t < kGqChunk; ++t) {
+        const int x = x0 + lane + kGqRows * t, k = x / cols, c = x % cols;
+        v[t] = x < cols * cols ? ue[(int64_t)(b0 + k) * in + b0 + c] : 0.f;
+      }
+#pragma unroll
+      for (int t = 0; t < kGqChunk; ++t) {
+        const int x = x0 + lane + kGqRows * t;
+        if (x < cols * cols) sm.ub[x / cols][x % cols] = v[t];
+      }
+    }
+    const int sb0 = b0 / a.sblock, nsb = (b0 + cols - 1) / a.sblock - sb0 + 1;   // nsb <= kGqScales
+    for (int q = 0; q < nsb; ++q) sm.ls[q][lane] = row ? sr[sb0 + q] : 1.f;
+    __syncthreads();
     for (int j = 0; j < cols; ++j) {
-      const float x = lw[j][lane];
-      const float s = sr[(b0 + j) / a.sblock];
+      const float x = sm.lw[j][lane];
+      const float s = sm.ls[(b0 + j) / a.sblock - sb0][lane];
       const float v = fminf(fmaxf(x / s, -1.0f), 1.0f);
       const float qv = level_at(nearest<L>(v, mid), levv) * s;
       if (row) qr[b0 + j] = qv;
-      const float* uj = ue + (int64_t)(b0 + j) * in + b0;
-      const float err = (x - qv) / uj[j];
-      lw[j][lane] = err;                 // column j is final: its slot keeps the error
-      for (int c = j + 1; c < cols; ++c) lw[c][lane] = lw[c][lane] - err * uj[c];
+      const float err = (x - qv) / sm.ub[j][j];
+      sm.lw[j][lane] = err;              // column j is final: its slot keeps the error
+      for (int c = j + 1; c < cols; ++c) sm.lw[c][lane] = sm.lw[c][lane] - err * sm.ub[j][c];
     }
-    // the later columns: w -= (errors of the block) . U[block rows, column], chained in order
-    for (int c0 = b0 + cols; c0 < a.in; c0 += kGqChunk) {
-      float acc[kGqChunk];
+    // the later columns: w -= (errors of the block) . U[block rows, column], chained in order;
+    // chunk c0's factor values and weights were requested while the previous chunk was applied
+    const int c_first = b0 + cols;
+    if (c_first < a.in) {
+      float fv[kGqChunkLoads], wv[kGqChunk];
+      chunk_load(fv, b0, cols, c_first);
+      row_load(wv, c_first);
+      int buf = 0;
+      for (int c0 = c_first; c0 < a.in; c0 += kGqChunk) {
+        chunk_store(fv, buf);
+        float wc[kGqChunk];
 #pragma unroll
-      for (int i = 0; i < kGqChunk; ++i) acc[i] = 0.f;
-      const int valid = min(kGqChunk, a.in - c0);
-      for (int k = 0; k < cols; ++k) {
-        const float ek = lw[k][lane];
-        const float* uk = ue + (int64_t)(b0 + k) * in + c0;
-        if (valid == kGqChunk) {
+        for (int i = 0; i < kGqChunk; ++i) wc[i] = wv[i];
+        __syncthreads();                 // this chunk's factor values are in LDS
+        if (c0 + kGqChunk < a.in) {      // (uniform) the next chunk, in flight during this one
+          chunk_load(fv, b0, cols, c0 + kGqChunk);
+          row_load(wv, c0 + kGqChunk);
+        }
+        float acc[kGqChunk];
 #pragma unroll
-          for (int i = 0; i < kGqChunk; ++i) acc[i] = __builtin_fmaf(ek, uk[i], acc[i]);
-        } else {
+        for (int i = 0; i < kGqChunk; ++i) acc[i] = 0.f;
+        for (int k = 0; k < cols; ++k) {
+          const float ek = sm.lw[k][lane];
+#pragma unroll
+          for (int i = 0; i < kGqChunk; ++i) acc[i] = __builtin_fmaf(ek, sm.uc[buf][k][i], acc[i]);
+        }
+        if (row) {
+          const int valid = min(kGqChunk, a.in - c0);
 #pragma unroll
           for (int i = 0; i < kGqChunk; ++i)
-            if (i < valid) acc[i] = __builtin_fmaf(ek, uk[i], acc[i]);
+            if (i < valid) wr[c0 + i] = wc[i] - acc[i];
         }
-      }
-      if (row) {
-#pragma unroll
-        for (int i = 0; i < kGqChunk; ++i)
-          if (i < valid) wr[c0 + i] = wr[c0 + i] - acc[i];
+        buf ^= 1;
       }
     }
+    __syncthreads();                     // the block's LDS is read out before the next block's
   }
-  // dead columns zeroed (q times 0, as the reference's mask product), then the table indices
+  // dead columns zeroed (q times 0, as the reference's mask product), then the table indices;
+  // 16 columns' loads at a time
   if (!row) return;
   uint8_t* cr = a.codes + ((int64_t)e * a.out + r) * in;
-  for (int c = 0; c < a.in; ++c) {
-    float qv = qr[c];
-    if (a.dead) qv = qv * (a.dead[(int64_t)e * in + c] ? 0.0f : 1.0f);
-    qr[c] = qv;
-    const float s = sr[c / a.sblock];
-    cr[c] = (uint8_t)nearest<L>(fminf(fmaxf(qv / s, -1.0f), 1.0f), mid);
+  for (int c0 = 0; c0 < a.in; c0 += kGqChunk) {
+    float qv[kGqChunk], sv[kGqChunk];
+    bool dd[kGqChunk];
+#pragma unroll
+    for (int i = 0; i < kGqChunk; ++i) {
+      const int c = min(c0 + i, a.in - 1);
+      qv[i] = qr[c];
+      sv[i] = sr[c / a.sblock];
+      dd[i] = a.dead ? a.dead[(int64_t)e * in + c] != 0 : false;
+    }
+#pragma unroll
+    for (int i = 0; i < kGqChunk; ++i) {
+      if (c0 + i < a.in) {
+        const float q = qv[i] * (dd[i] ? 0.0f : 1.0f);
+        qr[c0 + i] = a.dead ? q : qv[i];
+        cr[c0 + i] = (uint8_t)nearest<L>(fminf(fmaxf((a.dead ? q : qv[i]) / sv[i], -1.0f), 1.0f), mid);
+      }
+    }
   }
 }
 
@@ -284,6 +365,8 @@ extern "C" int bh_hex_gptq_sweep(float* w, const float* u, const float* levels, 
     return fail(BH_HEX_ERR_VALUE, std::string(who) + ": bad sizes (block 1..128, in a multiple of scale_block)");
   if (n > 65535 || out > (int64_t)65535 * kGqRows || in > (1 << 24))
     return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": too many experts, rows or columns");
+  if (scale_block < 32)   // a block's scales are staged for at most kGqScales scale blocks
+    return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": scale blocks of at least 32 inputs");
   if (n == 0 || out == 0) return BH_HEX_OK;
   if (!w || !u || !levels || !scale || !q || !codes) return fail(BH_HEX_ERR_VALUE, std::string(who) + ": null pointer");
   GptqArgs a{w, u, levels, scale, dead, q, codes, (int32_t)out, (int32_t)in, scale_block, block};

@@ -157,6 +157,9 @@ def test_sweep_kernel_argument_checks():
                           torch.ones(1, 4, 2, device=DEV))
     with pytest.raises(ValueError, match="on the GPU"):
         gptq.sweep_device(z.cpu(), torch.zeros(1, 64, 64), torch.zeros(1, 16), torch.ones(1, 4, 2))
+    with pytest.raises(NotImplementedError, match="at least 32 inputs"):
+        gptq.sweep_device(z, torch.zeros(1, 64, 64, device=DEV), torch.zeros(1, 16, device=DEV),
+                          torch.ones(1, 4, 4, device=DEV), 16)
 
 
 def test_gptq_config2_width_and_fused_kernels():
