@@ -200,9 +200,10 @@ __global__ __launch_bounds__(512, 2) void hex_gemm_kernel(MoeArgs a, int n_tiles
   // One step (phase P = st % D): the loads of step st + D - 1 first (into the ring stage and
   // register set that step st - 1 used; past the end the last step repeats, so every load
   // stays unconditional), then the math of this one:
-  // the two groups' 32 operands from the table, then per m-tile j the 4 activation fragments
-  // (those of j + 1 are read before the MFMAs of j) and two interleaved 4-deep MFMA chains,
-  // whose block partials are scaled into the accumulators one m-tile later.
+  // per half step (two k-slices) the groups' operands from the table, then per m-tile j the two
+  // activation fragments (those of j + 1 are read before the MFMAs of j) and per group a
+  // two-MFMA chain, whose block partial (128-input scales) is scaled into the accumulator one
+  // m-tile later (4-bit gate/up: at once); at 32-input scales each MFMA's partial is scaled.
   auto step = [&](int st, auto phase) {
     constexpr int P = decltype(phase)::value;
     const uint32_t* at = sm.atile[st % D];
@@ -238,6 +239,7 @@ __global__ __launch_bounds__(512, 2) void hex_gemm_kernel(MoeArgs a, int n_tiles
 #pragma unroll
         for (int q = 0; q < 2; ++q) bq[g][q] = lookup8<BITS, ES>(r[g][2 * hq + q], cb[g], tab);
       u32x4 av[2][2];
+      f32x4 pp[kMaxNG];                  // (SB 4) the previous m-tile's block partials
       afrag(0, hq, av[0]);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -253,14 +255,29 @@ __global__ __launch_bounds__(512, 2) void hex_gemm_kernel(MoeArgs a, int n_tiles
         __builtin_amdgcn_sched_barrier(0);
         const u32x4 (&x)[2] = av[j & 1];
         if constexpr (SB == 4) {
-          // the block's scale times the partial of each half step (one 128-input block per step)
+          // the block's scale times the partial of each half step (one 128-input block per step),
+          // added one m-tile later so that the multiply-adds run while this m-tile's MFMAs do
+          // (config 3: 420.0 -> 414.8 us per layer; the 4-bit gate/up kernel, two weight-row
+          // groups per wave, measured 5 us slower that way at config 5 and adds at once)
+          constexpr bool kLate = BITS == 3 || !GLU;
           f32x4 p[kMaxNG];
 #pragma unroll
           for (int g = 0; g < kNG; ++g) p[g] = mfma16x16x32<ADT>(x[0], bq[g][0], f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
           for (int g = 0; g < kNG; ++g) p[g] = mfma16x16x32<ADT>(x[1], bq[g][1], p[g]);
+          if constexpr (kLate) {
+            if (j > 0)
 #pragma unroll
-          for (int g = 0; g < kNG; ++g) acc[j][g] += p[g] * f[g][0];
+              for (int g = 0; g < kNG; ++g) acc[j - 1][g] += pp[g] * f[g][0];
+#pragma unroll
+            for (int g = 0; g < kNG; ++g) pp[g] = p[g];
+            if (j == 7)
+#pragma unroll
+              for (int g = 0; g < kNG; ++g) acc[7][g] += pp[g] * f[g][0];
+          } else {
+#pragma unroll
+            for (int g = 0; g < kNG; ++g) acc[j][g] += p[g] * f[g][0];
+          }
         } else {
           // each k-slice partial times its block's scale
 #pragma unroll
