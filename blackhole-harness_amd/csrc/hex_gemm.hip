@@ -6,10 +6,11 @@
 // writes the whole bf16 weight set and reads it back; here the packed indices go straight from
 // HBM to the matrix cores. The plan's expert blocks are 128 slots (block_m = 128).
 //
-//  * One workgroup (8 waves) per tile of 128 slots x 256 weight rows of one expert: down takes
-//    256 output rows; GLU takes 128 outputs, i.e. the same 128 rows of gate and of up. Each
-//    wave holds all 128 slots x 32 weight rows (two groups of 16; GLU: 16 gate and the same
-//    16 up rows) in 16 accumulator tiles, so every weight is decoded by exactly one wave.
+//  * One workgroup per tile of 128 slots x R weight rows of one expert (3 bits: 4 waves, R = 256;
+//    4 bits: 16 waves, R = 512): down takes R output rows; GLU takes R / 2 outputs, i.e. the
+//    same rows of gate and of up. Each wave holds all 128 slots x 16 NG weight rows (NG groups of
+//    16; GLU: half gate, half the same up rows) in accumulator tiles, so every weight is decoded
+//    by exactly one wave.
 //  * The inputs run in steps of 128 (4 HEX blocks, 4 MFMA k-slices). A step's activation tile
 //    (128 gathered slot rows x 128 inputs, 32 KB) is loaded once per workgroup and staged
 //    through a two-stage LDS ring in the MFMA's fragment order, so every fragment read is one
@@ -32,15 +33,18 @@
 namespace bh {
 
 // Weight-row groups of 16 per wave: 4 at 3 bits (4 waves per workgroup, two workgroups per
-// compute unit, every activation fragment read feeds 4 groups), 2 at 4 bits (8 waves: the
-// 64 KB 4-bit table leaves room for one workgroup, whose waves then cover each other's latency).
+// compute unit, every activation fragment read feeds 4 groups), 2 at 4 bits (16 waves: the
+// 64 KB 4-bit table leaves room for one workgroup, whose four waves per SIMD cover each other's
+// latency).
 constexpr int kMaxNG = 4, kMaxChunks = 8;
 template <int BITS>
 struct GemmShape {
   static constexpr int NG = BITS == 3 ? 4 : 2;     // weight-row groups of 16 per wave
-  static constexpr int WAVES = 16 / NG;            // waves of a workgroup (256 weight rows)
+  static constexpr int WAVES = BITS == 3 ? 4 : 16; // waves of a workgroup
   static constexpr int THREADS = WAVES * kWave;
+  static constexpr int ROWS = WAVES * NG * 16;     // weight rows of a workgroup
   static constexpr int CHUNKS = 32 / WAVES;        // 1 KB chunks of a step's activation tile per wave
+  static constexpr int MINW = BITS == 3 ? 2 : 4;   // waves per SIMD (3 bits: two workgroups)
 };
 constexpr int kGM = 128;                // slots of a tile: one expert block of the plan
 constexpr int kGK = 128;                // inputs per pipeline step
@@ -51,17 +55,19 @@ constexpr int kXcds = 8;
 // vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima)
 constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
-template <bool GLU>
-constexpr int gemm_cols() { return GLU ? 128 : 256; }   // outputs of a tile
+template <int BITS, bool GLU>
+constexpr int gemm_cols() { return GLU ? GemmShape<BITS>::ROWS / 2 : GemmShape<BITS>::ROWS; }   // outputs of a tile
 
 template <int BITS, int ADT, bool GLU, int SB>
-__global__ __launch_bounds__(512, 2) void hex_gemm_kernel(MoeArgs a, int n_tiles) {
+__global__ __launch_bounds__(GemmShape<BITS>::THREADS, GemmShape<BITS>::MINW) void hex_gemm_kernel(MoeArgs a,
+                                                                                                   int n_tiles) {
   // (arrays below are sized by the non-dependent maxima kMaxNG / kMaxChunks: with sizes that
   // depend on BITS this compiler emits no host-side launch stub for the kernel)
   constexpr int kNG = GemmShape<BITS>::NG;
   constexpr int kGWaves = GemmShape<BITS>::WAVES;
   constexpr int kGThreads = GemmShape<BITS>::THREADS;
   constexpr int kChunks = GemmShape<BITS>::CHUNKS;
+  constexpr int kCols = gemm_cols<BITS, GLU>();
   constexpr int L = 1 << BITS;
   constexpr int NPAIR = 1 << (2 * BITS);
   constexpr int NM = GLU ? 2 : 1;
@@ -134,8 +140,8 @@ __global__ __launch_bounds__(512, 2) void hex_gemm_kernel(MoeArgs a, int n_tiles
     xo[i] = s < a.num_slots ? (uint32_t)((int64_t)(s / a.a_div) * a.s_xm * 2) + ((c & 3) * 32 + lg * 8) * 2 : kOOR;
   }
   // Weights: the wave's groups of 16 rows; lane (ln, lg) reads block lg of the step of row ln.
-  // Down: rows 256 nt + 16 (NG wave + g). GLU: group g is gate (g < NG/2) or up, half h = g % (NG/2):
-  // rows 128 nt + 16 (NG/2 wave + h) of both, so a lane holds gate and up of the same outputs.
+  // Down: rows R nt + 16 (NG wave + g). GLU: group g is gate (g < NG/2) or up, half h = g % (NG/2):
+  // rows R/2 nt + 16 (NG/2 wave + h) of both, so a lane holds gate and up of the same outputs.
   constexpr int HG = kNG / 2;
   uint32_t vw[kMaxNG], vb[kMaxNG];
   uint32_t cb[kMaxNG];
@@ -146,7 +152,7 @@ __global__ __launch_bounds__(512, 2) void hex_gemm_kernel(MoeArgs a, int n_tiles
     const bh_hex_proj& w = m ? a.w1 : a.w0;
     rw[g] = buffer_rsrc(w.idx + (int64_t)e * w.s_ie, (int64_t)a.N * w.s_in * 4);
     rb[g] = buffer_rsrc(w.block_scale + (int64_t)e * w.s_be, (int64_t)a.N * w.s_bn);
-    const int n = GLU ? nt * 128 + (wave * HG + g % HG) * 16 + ln : nt * 256 + (wave * kNG + g) * 16 + ln;
+    const int n = GLU ? nt * kCols + (wave * HG + g % HG) * 16 + ln : nt * kCols + (wave * kNG + g) * 16 + ln;
     vw[g] = n < a.N ? (uint32_t)((int64_t)n * w.s_in * 4) + lg * BLKB : kOOR;
     vb[g] = n < a.N ? (uint32_t)((int64_t)n * w.s_bn) : kOOR;
     cb[g] = GLU ? (uint32_t)m * (TC * 2) + (lane & (TC / 2 - 1)) * 4u : (lane & (TC - 1)) * 4u;
@@ -257,9 +263,9 @@ __global__ __launch_bounds__(512, 2) void hex_gemm_kernel(MoeArgs a, int n_tiles
         if constexpr (SB == 4) {
           // the block's scale times the partial of each half step (one 128-input block per step),
           // added one m-tile later so that the multiply-adds run while this m-tile's MFMAs do
-          // (config 3: 420.0 -> 414.8 us per layer; the 4-bit gate/up kernel, two weight-row
-          // groups per wave, measured 5 us slower that way at config 5 and adds at once)
-          constexpr bool kLate = BITS == 3 || !GLU;
+          // (config 3: 420.0 -> 414.8 us per layer; the 4-bit kernels, two weight-row groups per
+          // wave and at most 128 registers, add at once)
+          constexpr bool kLate = BITS == 3;
           f32x4 p[kMaxNG];
 #pragma unroll
           for (int g = 0; g < kNG; ++g) p[g] = mfma16x16x32<ADT>(x[0], bq[g][0], f32x4{0.f, 0.f, 0.f, 0.f});
@@ -303,94 +309,102 @@ __global__ __launch_bounds__(512, 2) void hex_gemm_kernel(MoeArgs a, int n_tiles
   if (st < nst) step(st, std::integral_constant<int, 0>());
 
   // ---- epilogue (reference order: acc * es; silu(g) * (u * es_u); * topk weight). The
-  // outputs go through the (now free) activation ring so that each slot row is written with
-  // 16-byte stores: GLU's 128 x 128 tile at once (rows of 136 halves), down's 128 x 256 floats
-  // in two halves of 64 slots (rows of 260 floats); the padding staggers the banks.
+  // outputs go through the (now free) activation ring, 64 KB, so that each slot row is written
+  // with 16-byte stores, in passes of PR slot rows: GLU's tile in rows of kCols + 8 halves (the
+  // padding staggers the banks); down's y in rows of kCols values whose 16-value column groups
+  // are XORed with row bits 2-3 (the four row groups of a write land in distinct banks).
   const float es0 = a.w0.expert_scale[e], es1 = a.w1.expert_scale[e];
   uint32_t* const stage = sm.atile[0];                   // stages 0 and 1: 64 KB in a row
+  auto at_rc = [](int row, int col) { return row * kCols + (col ^ (((row >> 2) & 3) << 4)); };
   if constexpr (GLU) {
-    constexpr int RS = 136;                              // halves per staged row
+    constexpr int RS = kCols + 8;                        // halves per staged row
+    constexpr int PR = 32768 / RS >= kGM ? kGM : kGM / 2;
+    constexpr int TPR = kCols / 8;                       // threads per row, 8 outputs (16 bytes) each
     uint16_t* const st16 = reinterpret_cast<uint16_t*>(stage);
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+    for (int p = 0; p < kGM / PR; ++p) {
+      if (p) __syncthreads();                            // the previous pass's readers are done
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
+      for (int j = p * (PR / 16); j < (p + 1) * (PR / 16); ++j)
 #pragma unroll
-        for (int h = 0; h < HG; ++h) {
-          const float gt = acc[j][h][r] * es0;
-          const float hv = gt * __builtin_amdgcn_rcpf(1.0f + __expf(-gt)) * (acc[j][HG + h][r] * es1);
-          st16[(j * 16 + 4 * lg + r) * RS + (wave * HG + h) * 16 + ln] = (uint16_t)to_bits<ADT>(hv);
+        for (int r = 0; r < 4; ++r) {
+#pragma unroll
+          for (int h = 0; h < HG; ++h) {
+            const float gt = acc[j][h][r] * es0;
+            const float hv = gt * __builtin_amdgcn_rcpf(1.0f + __expf(-gt)) * (acc[j][HG + h][r] * es1);
+            st16[(j * 16 + 4 * lg + r - p * PR) * RS + (wave * HG + h) * 16 + ln] = (uint16_t)to_bits<ADT>(hv);
+          }
         }
-      }
-    __syncthreads();
-    // 16 threads per row, 8 outputs (16 bytes) each
+      __syncthreads();
 #pragma unroll
-    for (int it = 0; it < kGM * 16 / kGThreads; ++it) {
-      const int row = it * (kGThreads / 16) + tid / 16, c = (tid & 15) * 8;
-      const int slot = slots[row], col = nt * 128 + c;
-      if (slot >= a.num_slots || col >= a.N) continue;
-      uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + (int64_t)slot * a.s_om + col;
-      const u32x4 v = *reinterpret_cast<const u32x4*>(st16 + row * RS + c);
-      if (col + 8 <= a.N) {
-        *reinterpret_cast<u32x4*>(dst) = v;
-      } else {
-        for (int q = 0; q < a.N - col; ++q) dst[q] = st16[row * RS + c + q];
+      for (int it = 0; it < PR * TPR / kGThreads; ++it) {
+        const int row = it * (kGThreads / TPR) + tid / TPR, c = (tid % TPR) * 8;
+        const int slot = slots[p * PR + row], col = nt * kCols + c;
+        if (slot >= a.num_slots || col >= a.N) continue;
+        uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + (int64_t)slot * a.s_om + col;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(st16 + row * RS + c);
+        if (col + 8 <= a.N) {
+          *reinterpret_cast<u32x4*>(dst) = v;
+        } else {
+          for (int q = 0; q < a.N - col; ++q) dst[q] = st16[row * RS + c + q];
+        }
       }
     }
   } else if (a.y16) {
-    // y in the activation dtype: the whole 128 x 256 tile fills the 64 KB. Column bits 4-5 are
-    // XORed with row bits 2-3 (the four row groups of a write land in distinct banks; 8-half
-    // chunks stay contiguous).
+    // y in the activation dtype
+    constexpr int PR = 32768 / kCols;                    // slot rows per pass
+    constexpr int TPR = kCols / 8;
     uint16_t* const st16 = reinterpret_cast<uint16_t*>(stage);
-    auto at_rc = [](int row, int col) { return row * 256 + (col ^ (((row >> 2) & 3) << 4)); };
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+    for (int p = 0; p < kGM / PR; ++p) {
+      if (p) __syncthreads();
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = j * 16 + 4 * lg + r;
-        const float w = slot_w[row];
+      for (int j = p * (PR / 16); j < (p + 1) * (PR / 16); ++j)
 #pragma unroll
-        for (int g = 0; g < kNG; ++g)
-          st16[at_rc(row, (wave * kNG + g) * 16 + ln)] = (uint16_t)to_bits<ADT>(acc[j][g][r] * es0 * w);
-      }
-    __syncthreads();
-    // 32 threads per row, 8 outputs (16 bytes) each
+        for (int r = 0; r < 4; ++r) {
+          const int row = j * 16 + 4 * lg + r - p * PR;  // within the pass
+          const float w = slot_w[p * PR + row];
 #pragma unroll
-    for (int it = 0; it < kGM * 32 / kGThreads; ++it) {
-      const int row = it * (kGThreads / 32) + tid / 32, c = (tid & 31) * 8;
-      const int slot = slots[row], col = nt * 256 + c;
-      if (slot >= a.num_slots || col >= a.N) continue;
-      uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + (int64_t)slot * a.s_om + col;
-      const u32x4 v = *reinterpret_cast<const u32x4*>(st16 + at_rc(row, c));
-      if (col + 8 <= a.N) {
-        *reinterpret_cast<u32x4*>(dst) = v;
-      } else {
-        for (int q = 0; q < a.N - col; ++q) dst[q] = st16[at_rc(row, c) + q];
+          for (int g = 0; g < kNG; ++g)
+            st16[at_rc(row, (wave * kNG + g) * 16 + ln)] = (uint16_t)to_bits<ADT>(acc[j][g][r] * es0 * w);
+        }
+      __syncthreads();
+#pragma unroll
+      for (int it = 0; it < PR * TPR / kGThreads; ++it) {
+        const int row = it * (kGThreads / TPR) + tid / TPR, c = (tid % TPR) * 8;
+        const int slot = slots[p * PR + row], col = nt * kCols + c;
+        if (slot >= a.num_slots || col >= a.N) continue;
+        uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + (int64_t)slot * a.s_om + col;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(st16 + at_rc(row, c));
+        if (col + 8 <= a.N) {
+          *reinterpret_cast<u32x4*>(dst) = v;
+        } else {
+          for (int q = 0; q < a.N - col; ++q) dst[q] = st16[at_rc(row, c) + q];
+        }
       }
     }
   } else {
-    // 64 rows of 256 floats fill the 64 KB exactly: instead of padding, column bits 4-5 are
-    // XORed with row bits 2-3 (conflict-free writes; 4-float chunks stay contiguous)
+    // float32 y
+    constexpr int PR = 16384 / kCols;                    // slot rows per pass
+    constexpr int TPR = kCols / 4;                       // threads per row, 4 outputs (16 bytes) each
     float* const stf = reinterpret_cast<float*>(stage);
-    auto at_rc = [](int row, int col) { return row * 256 + (col ^ (((row >> 2) & 3) << 4)); };
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      if (h) __syncthreads();                            // the first half's readers are done
+    for (int p = 0; p < kGM / PR; ++p) {
+      if (p) __syncthreads();
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = p * (PR / 16); j < (p + 1) * (PR / 16); ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int row = j * 16 + 4 * lg + r;           // within the half
-          const float w = slot_w[h * 64 + row];
+          const int row = j * 16 + 4 * lg + r - p * PR;
+          const float w = slot_w[p * PR + row];
 #pragma unroll
-          for (int g = 0; g < kNG; ++g) stf[at_rc(row, (wave * kNG + g) * 16 + ln)] = acc[h * 4 + j][g][r] * es0 * w;
+          for (int g = 0; g < kNG; ++g) stf[at_rc(row, (wave * kNG + g) * 16 + ln)] = acc[j][g][r] * es0 * w;
         }
       __syncthreads();
-      // 64 threads per row, 4 outputs (16 bytes) each
 #pragma unroll
-      for (int it = 0; it < 64 * 64 / kGThreads; ++it) {
-        const int row = it * (kGThreads / 64) + tid / 64, c = (tid & 63) * 4;
-        const int slot = slots[h * 64 + row], col = nt * 256 + c;
+      for (int it = 0; it < PR * TPR / kGThreads; ++it) {
+        const int row = it * (kGThreads / TPR) + tid / TPR, c = (tid % TPR) * 4;
+        const int slot = slots[p * PR + row], col = nt * kCols + c;
         if (slot >= a.num_slots || col >= a.N) continue;
         float* dst = reinterpret_cast<float*>(a.out) + (int64_t)slot * a.s_om + col;
         const f32x4 v = *reinterpret_cast<const f32x4*>(stf + at_rc(row, c));
@@ -445,7 +459,9 @@ int gemm_run(const char* who, bool glu, int bits, int adt, int sb, const MoeArgs
     return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": block_m 128 needs 16-byte aligned output rows");
   const int64_t x_rows = cdiv(a.num_slots, a.a_div);
   if (x_rows * a.s_xm * 2 > kMaxRecords) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": activations over 2 GiB");
-  const int64_t n_tiles = cdiv(a.N, glu ? gemm_cols<true>() : gemm_cols<false>());
+  const int cols = bits == 4 ? (glu ? gemm_cols<4, true>() : gemm_cols<4, false>())
+                             : (glu ? gemm_cols<3, true>() : gemm_cols<3, false>());
+  const int64_t n_tiles = cdiv(a.N, cols);
   const int64_t wgs = num_blocks * n_tiles;
   if (wgs > INT32_MAX) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": plan too large");
   if (wgs == 0) return BH_HEX_OK;
