@@ -39,12 +39,17 @@ namespace bh {
 constexpr int kMaxNG = 4, kMaxChunks = 8;
 template <int BITS>
 struct GemmShape {
-  static constexpr int NG = BITS == 3 ? 4 : 2;     // weight-row groups of 16 per wave
-  static constexpr int WAVES = BITS == 3 ? 4 : 16; // waves of a workgroup
+  // 4 bits: 16 waves of two groups each (one workgroup per compute unit, four waves per SIMD at
+  // 128 registers: config 5 T=2048 1106 -> 943 us against 8 waves). 3 bits: 4 waves of four groups
+  // (two workgroups per compute unit, two waves per SIMD); the 16-wave shape measured slower there
+  // (config 3: 424 -> 433 us), its fragment reads feeding two groups instead of four.
+  static constexpr bool WIDE = BITS == 4;
+  static constexpr int NG = WIDE ? 2 : 4;          // weight-row groups of 16 per wave
+  static constexpr int WAVES = WIDE ? 16 : 4;      // waves of a workgroup
   static constexpr int THREADS = WAVES * kWave;
   static constexpr int ROWS = WAVES * NG * 16;     // weight rows of a workgroup
   static constexpr int CHUNKS = 32 / WAVES;        // 1 KB chunks of a step's activation tile per wave
-  static constexpr int MINW = BITS == 3 ? 2 : 4;   // waves per SIMD (3 bits: two workgroups)
+  static constexpr int MINW = WIDE ? 4 : 2;        // waves per SIMD (narrow: two workgroups)
 };
 constexpr int kGM = 128;                // slots of a tile: one expert block of the plan
 constexpr int kGK = 128;                // inputs per pipeline step
@@ -76,8 +81,8 @@ __global__ __launch_bounds__(GemmShape<BITS>::THREADS, GemmShape<BITS>::MINW) vo
   // Pair-table copies per entry: 64 at 4 bits; 32 at 3 bits, so that two workgroups fit in a
   // compute unit's LDS (a wave's table reads go to the banks in two halves of 32 lanes, so 32
   // copies keep down's reads conflict-free; GLU's gate and up tables get 16 copies each).
-  constexpr int TC = BITS == 3 ? 32 : 64;
-  constexpr int ES = BITS == 3 ? 7 : 8;          // log2 of an entry's bytes
+  constexpr int TC = GemmShape<BITS>::WIDE || BITS == 4 ? 64 : 32;
+  constexpr int ES = TC == 64 ? 8 : 7;           // log2 of an entry's bytes
   // Activation ring depth: tiles are loaded one step ahead of the math, as are the weight
   // words (two register sets). (Two steps ahead measured no faster.)
   constexpr int D = 2;
@@ -265,7 +270,7 @@ __global__ __launch_bounds__(GemmShape<BITS>::THREADS, GemmShape<BITS>::MINW) vo
           // added one m-tile later so that the multiply-adds run while this m-tile's MFMAs do
           // (config 3: 420.0 -> 414.8 us per layer; the 4-bit kernels, two weight-row groups per
           // wave and at most 128 registers, add at once)
-          constexpr bool kLate = BITS == 3;
+          constexpr bool kLate = !GemmShape<BITS>::WIDE;
           f32x4 p[kMaxNG];
 #pragma unroll
           for (int g = 0; g < kNG; ++g) p[g] = mfma16x16x32<ADT>(x[0], bq[g][0], f32x4{0.f, 0.f, 0.f, 0.f});
