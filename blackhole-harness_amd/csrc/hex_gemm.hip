@@ -32,24 +32,26 @@
 
 namespace bh {
 
-// Weight-row groups of 16 per wave: 4 at 3 bits (4 waves per workgroup, two workgroups per
-// compute unit, every activation fragment read feeds 4 groups), 2 at 4 bits (16 waves: the
-// 64 KB 4-bit table leaves room for one workgroup, whose four waves per SIMD cover each other's
-// latency).
+// The workgroup's shape, by bit width and scale block (SB 4: one fp8 scale per 128 inputs,
+// SB 1: per 32). Four waves per SIMD where the registers allow: two weight-row groups of 16 per
+// wave, at most 128 registers.
+//  * 4 bits: 16 waves (one workgroup per compute unit: the 64 KB pair table) measured against 8
+//    waves of two groups (two waves per SIMD): config 5 T=2048 1106 -> 943 us.
+//  * 3 bits, SB 4: 8 waves, two workgroups per compute unit, against 4 waves of four groups (two
+//    waves per SIMD, every activation fragment read feeding four groups, each m-tile's partials
+//    scaled behind the next m-tile's MFMAs): config 3 427.8 -> 424.4 us over four runs. 16 waves
+//    of two groups, one workgroup per compute unit, measured 424 -> 433 us.
+//  * 3 bits, SB 1: 4 waves of four groups; the 8-wave shape spills there (config 3 with 32-input
+//    scales 503 -> 532 us).
 constexpr int kMaxNG = 4, kMaxChunks = 8;
-template <int BITS>
+template <int BITS, int SB>
 struct GemmShape {
-  // 4 bits: 16 waves of two groups each (one workgroup per compute unit, four waves per SIMD at
-  // 128 registers: config 5 T=2048 1106 -> 943 us against 8 waves). 3 bits: 4 waves of four groups
-  // (two workgroups per compute unit, two waves per SIMD); the 16-wave shape measured slower there
-  // (config 3: 424 -> 433 us), its fragment reads feeding two groups instead of four.
-  static constexpr bool WIDE = BITS == 4;
-  static constexpr int NG = WIDE ? 2 : 4;          // weight-row groups of 16 per wave
-  static constexpr int WAVES = WIDE ? 16 : 4;      // waves of a workgroup
+  static constexpr int WAVES = BITS == 4 ? 16 : (SB == 4 ? 8 : 4);   // waves of a workgroup
+  static constexpr int NG = WAVES == 4 ? 4 : 2;    // weight-row groups of 16 per wave
   static constexpr int THREADS = WAVES * kWave;
-  static constexpr int ROWS = WAVES * NG * 16;     // weight rows of a workgroup
+  static constexpr int ROWS = WAVES * NG * 16;     // weight rows of a workgroup (256, or 512 at 4 bits)
   static constexpr int CHUNKS = 32 / WAVES;        // 1 KB chunks of a step's activation tile per wave
-  static constexpr int MINW = WIDE ? 4 : 2;        // waves per SIMD (narrow: two workgroups)
+  static constexpr int MINW = NG == 2 ? 4 : 2;     // waves per SIMD
 };
 constexpr int kGM = 128;                // slots of a tile: one expert block of the plan
 constexpr int kGK = 128;                // inputs per pipeline step
@@ -60,19 +62,19 @@ constexpr int kXcds = 8;
 // vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima)
 constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
-template <int BITS, bool GLU>
-constexpr int gemm_cols() { return GLU ? GemmShape<BITS>::ROWS / 2 : GemmShape<BITS>::ROWS; }   // outputs of a tile
+template <int BITS, int SB, bool GLU>
+constexpr int gemm_cols() { return GLU ? GemmShape<BITS, SB>::ROWS / 2 : GemmShape<BITS, SB>::ROWS; }   // outputs of a tile
 
 template <int BITS, int ADT, bool GLU, int SB>
-__global__ __launch_bounds__(GemmShape<BITS>::THREADS, GemmShape<BITS>::MINW) void hex_gemm_kernel(MoeArgs a,
+__global__ __launch_bounds__((GemmShape<BITS, SB>::THREADS), (GemmShape<BITS, SB>::MINW)) void hex_gemm_kernel(MoeArgs a,
                                                                                                    int n_tiles) {
   // (arrays below are sized by the non-dependent maxima kMaxNG / kMaxChunks: with sizes that
   // depend on BITS this compiler emits no host-side launch stub for the kernel)
-  constexpr int kNG = GemmShape<BITS>::NG;
-  constexpr int kGWaves = GemmShape<BITS>::WAVES;
-  constexpr int kGThreads = GemmShape<BITS>::THREADS;
-  constexpr int kChunks = GemmShape<BITS>::CHUNKS;
-  constexpr int kCols = gemm_cols<BITS, GLU>();
+  constexpr int kNG = GemmShape<BITS, SB>::NG;
+  constexpr int kGWaves = GemmShape<BITS, SB>::WAVES;
+  constexpr int kGThreads = GemmShape<BITS, SB>::THREADS;
+  constexpr int kChunks = GemmShape<BITS, SB>::CHUNKS;
+  constexpr int kCols = gemm_cols<BITS, SB, GLU>();
   constexpr int L = 1 << BITS;
   constexpr int NPAIR = 1 << (2 * BITS);
   constexpr int NM = GLU ? 2 : 1;
@@ -81,7 +83,7 @@ __global__ __launch_bounds__(GemmShape<BITS>::THREADS, GemmShape<BITS>::MINW) vo
   // Pair-table copies per entry: 64 at 4 bits; 32 at 3 bits, so that two workgroups fit in a
   // compute unit's LDS (a wave's table reads go to the banks in two halves of 32 lanes, so 32
   // copies keep down's reads conflict-free; GLU's gate and up tables get 16 copies each).
-  constexpr int TC = GemmShape<BITS>::WIDE || BITS == 4 ? 64 : 32;
+  constexpr int TC = BITS == 4 ? 64 : 32;
   constexpr int ES = TC == 64 ? 8 : 7;           // log2 of an entry's bytes
   // Activation ring depth: tiles are loaded one step ahead of the math, as are the weight
   // words (two register sets). (Two steps ahead measured no faster.)
@@ -250,7 +252,6 @@ __global__ __launch_bounds__(GemmShape<BITS>::THREADS, GemmShape<BITS>::MINW) vo
 #pragma unroll
         for (int q = 0; q < 2; ++q) bq[g][q] = lookup8<BITS, ES>(r[g][2 * hq + q], cb[g], tab);
       u32x4 av[2][2];
-      f32x4 pp[kMaxNG];                  // (SB 4) the previous m-tile's block partials
       afrag(0, hq, av[0]);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -266,29 +267,14 @@ __global__ __launch_bounds__(GemmShape<BITS>::THREADS, GemmShape<BITS>::MINW) vo
         __builtin_amdgcn_sched_barrier(0);
         const u32x4 (&x)[2] = av[j & 1];
         if constexpr (SB == 4) {
-          // the block's scale times the partial of each half step (one 128-input block per step),
-          // added one m-tile later so that the multiply-adds run while this m-tile's MFMAs do
-          // (config 3: 420.0 -> 414.8 us per layer; the 4-bit kernels, two weight-row groups per
-          // wave and at most 128 registers, add at once)
-          constexpr bool kLate = !GemmShape<BITS>::WIDE;
+          // the block's scale times the partial of each half step (one 128-input block per step)
           f32x4 p[kMaxNG];
 #pragma unroll
           for (int g = 0; g < kNG; ++g) p[g] = mfma16x16x32<ADT>(x[0], bq[g][0], f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
           for (int g = 0; g < kNG; ++g) p[g] = mfma16x16x32<ADT>(x[1], bq[g][1], p[g]);
-          if constexpr (kLate) {
-            if (j > 0)
 #pragma unroll
-              for (int g = 0; g < kNG; ++g) acc[j - 1][g] += pp[g] * f[g][0];
-#pragma unroll
-            for (int g = 0; g < kNG; ++g) pp[g] = p[g];
-            if (j == 7)
-#pragma unroll
-              for (int g = 0; g < kNG; ++g) acc[7][g] += pp[g] * f[g][0];
-          } else {
-#pragma unroll
-            for (int g = 0; g < kNG; ++g) acc[j][g] += p[g] * f[g][0];
-          }
+          for (int g = 0; g < kNG; ++g) acc[j][g] += p[g] * f[g][0];
         } else {
           // each k-slice partial times its block's scale
 #pragma unroll
@@ -427,9 +413,10 @@ __global__ __launch_bounds__(GemmShape<BITS>::THREADS, GemmShape<BITS>::MINW) vo
 
 template <int BITS, int ADT, bool GLU>
 static void gemm_sb(int sb, dim3 grid, hipStream_t st, const MoeArgs& a, int n_tiles) {
-  const dim3 block(GemmShape<BITS>::THREADS);
-  if (sb == 1) hipLaunchKernelGGL((hex_gemm_kernel<BITS, ADT, GLU, 1>), grid, block, 0, st, a, n_tiles);
-  else hipLaunchKernelGGL((hex_gemm_kernel<BITS, ADT, GLU, 4>), grid, block, 0, st, a, n_tiles);
+  if (sb == 1)
+    hipLaunchKernelGGL((hex_gemm_kernel<BITS, ADT, GLU, 1>), grid, dim3(GemmShape<BITS, 1>::THREADS), 0, st, a, n_tiles);
+  else
+    hipLaunchKernelGGL((hex_gemm_kernel<BITS, ADT, GLU, 4>), grid, dim3(GemmShape<BITS, 4>::THREADS), 0, st, a, n_tiles);
 }
 
 template <bool GLU>
@@ -464,8 +451,11 @@ int gemm_run(const char* who, bool glu, int bits, int adt, int sb, const MoeArgs
     return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": block_m 128 needs 16-byte aligned output rows");
   const int64_t x_rows = cdiv(a.num_slots, a.a_div);
   if (x_rows * a.s_xm * 2 > kMaxRecords) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": activations over 2 GiB");
-  const int cols = bits == 4 ? (glu ? gemm_cols<4, true>() : gemm_cols<4, false>())
-                             : (glu ? gemm_cols<3, true>() : gemm_cols<3, false>());
+  // (a tile's outputs do not depend on the scale block: both 3-bit shapes cover 256 weight rows)
+  static_assert(gemm_cols<3, 1, false>() == gemm_cols<3, 4, false>() && gemm_cols<4, 1, false>() == gemm_cols<4, 4, false>(),
+                "tile widths per bit width");
+  const int cols = bits == 4 ? (glu ? gemm_cols<4, 4, true>() : gemm_cols<4, 4, false>())
+                             : (glu ? gemm_cols<3, 4, true>() : gemm_cols<3, 4, false>());
   const int64_t n_tiles = cdiv(a.N, cols);
   const int64_t wgs = num_blocks * n_tiles;
   if (wgs > INT32_MAX) return fail(BH_HEX_ERR_UNSUPPORTED, std::string(who) + ": plan too large");
