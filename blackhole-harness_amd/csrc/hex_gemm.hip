@@ -6,9 +6,9 @@
 // writes the whole bf16 weight set and reads it back; here the packed indices go straight from
 // HBM to the matrix cores. The plan's expert blocks are 128 slots (block_m = 128).
 //
-//  * One workgroup per tile of 128 slots x R weight rows of one expert (3 bits: 4 waves, R = 256;
-//    4 bits: 16 waves, R = 512): down takes R output rows; GLU takes R / 2 outputs, i.e. the
-//    same rows of gate and of up. Each wave holds all 128 slots x 16 NG weight rows (NG groups of
+//  * One workgroup per tile of 128 slots x R weight rows of one expert (R = 256 at 3 bits, 512 at
+//    4 bits; the workgroup's waves per GemmShape below): down takes R output rows; GLU takes R / 2
+//    outputs, i.e. the same rows of gate and of up. Each wave holds all 128 slots x 16 NG weight rows (NG groups of
 //    16; GLU: half gate, half the same up rows) in accumulator tiles, so every weight is decoded
 //    by exactly one wave.
 //  * The inputs run in steps of 128 (4 HEX blocks, 4 MFMA k-slices). A step's activation tile
