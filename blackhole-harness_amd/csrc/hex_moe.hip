@@ -34,6 +34,59 @@ __device__ __forceinline__ f32x4 y4(const void* y, int64_t at) {
   }
 }
 
+// Eight 16-bit y values of a slot row (one 16-byte load) as two float32 quads.
+template <int YDT>
+__device__ __forceinline__ void y8(const void* y, int64_t at, f32x4& lo, f32x4& hi) {
+  const u32x4 v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(y) + at);
+  lo = f32x4{from_bits<YDT>(v[0] & 0xFFFFu), from_bits<YDT>(v[0] >> 16), from_bits<YDT>(v[1] & 0xFFFFu),
+             from_bits<YDT>(v[1] >> 16)};
+  hi = f32x4{from_bits<YDT>(v[2] & 0xFFFFu), from_bits<YDT>(v[2] >> 16), from_bits<YDT>(v[3] & 0xFFFFu),
+             from_bits<YDT>(v[3] >> 16)};
+}
+
+// 16-bit y in rows of multiples of 8 values: eight outputs per thread, each slot row read with
+// one 16-byte load (the four-output kernel below reads 8 bytes per load). The same sums in the
+// same order.
+template <int ODT, int IDT, int YDT>
+__global__ __launch_bounds__(256) void moe_reduce8_kernel(const void* __restrict__ y, int64_t s_ym,
+                                                          const void* __restrict__ ids, int32_t n_experts, int32_t k,
+                                                          int64_t H, void* __restrict__ out, int64_t s_ot) {
+  const int64_t t = blockIdx.y;
+  const int64_t h = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (h >= H) return;
+  f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
+  for (int j0 = 0; j0 < k; j0 += 8) {
+    int64_t id[8];
+    f32x4 v0[8], v1[8];
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const int64_t s = t * k + j0 + d;
+      if (j0 + d < k) {
+        if constexpr (IDT == BH_HEX_I64) id[d] = reinterpret_cast<const int64_t*>(ids)[s];
+        else id[d] = reinterpret_cast<const int32_t*>(ids)[s];
+        y8<YDT>(y, s * s_ym + h, v0[d], v1[d]);
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < 8; ++d)
+      if (j0 + d < k && id[d] >= 0 && id[d] < n_experts) {
+        a0 += v0[d];
+        a1 += v1[d];
+      }
+  }
+  if constexpr (ODT == BH_HEX_F32) {
+    *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(out) + t * s_ot + h) = a0;
+    *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(out) + t * s_ot + h + 4) = a1;
+  } else {
+    u32x4 v;
+    v[0] = to_bits<ODT>(a0[0]) | (to_bits<ODT>(a0[1]) << 16);
+    v[1] = to_bits<ODT>(a0[2]) | (to_bits<ODT>(a0[3]) << 16);
+    v[2] = to_bits<ODT>(a1[0]) | (to_bits<ODT>(a1[1]) << 16);
+    v[3] = to_bits<ODT>(a1[2]) | (to_bits<ODT>(a1[3]) << 16);
+    *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(out) + t * s_ot + h) = v;
+  }
+}
+
 template <int ODT, int IDT, int YDT>
 __global__ __launch_bounds__(256) void moe_reduce_kernel(const void* __restrict__ y, int64_t s_ym,
                                                          const void* __restrict__ ids, int32_t n_experts, int32_t k,
@@ -452,6 +505,19 @@ extern "C" int bh_hex_moe_workspace(int64_t num_blocks, int64_t n_out, int64_t n
 template <int ODT, int IDT>
 static void reduce_ydt(int ydt, dim3 grid, hipStream_t st, const void* y, int64_t s_ym, const void* ids,
                        int32_t n_experts, int32_t k, int64_t H, void* out, int64_t s_ot) {
+  // 16-bit y in 16-byte aligned rows of multiples of 8 values: the eight-output kernel
+  const bool wide = ydt != BH_HEX_F32 && H % 8 == 0 && s_ym % 8 == 0 && s_ot % 8 == 0 && aligned(y, 16) &&
+                    aligned(out, 16);
+  if (wide) {
+    const dim3 g8((unsigned)cdiv(H, 2048), grid.y);
+    if (ydt == BH_HEX_BF16)
+      hipLaunchKernelGGL((moe_reduce8_kernel<ODT, IDT, BH_HEX_BF16>), g8, dim3(256), 0, st, y, s_ym, ids, n_experts, k,
+                         H, out, s_ot);
+    else
+      hipLaunchKernelGGL((moe_reduce8_kernel<ODT, IDT, BH_HEX_F16>), g8, dim3(256), 0, st, y, s_ym, ids, n_experts, k,
+                         H, out, s_ot);
+    return;
+  }
   if (ydt == BH_HEX_F32)
     hipLaunchKernelGGL((moe_reduce_kernel<ODT, IDT, BH_HEX_F32>), grid, dim3(256), 0, st, y, s_ym, ids, n_experts, k, H,
                        out, s_ot);
