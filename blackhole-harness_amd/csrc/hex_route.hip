@@ -335,12 +335,16 @@ __global__ __launch_bounds__(kAlignThreads) void align_place_kernel(const void* 
   __syncthreads();
   const int key = (id >= 0 && id < n && (!TIER || lk[TIER ? id : 0] >= 0)) ? (int)id : n;
   // thread e: expert e's slots in earlier chunks and in all (n <= kAlignThreads)
-  int tot = 0;
+  // (no store inside the loop, so its reads are issued together)
+  int tot = 0, mine = 0;
   if (tid < n) {
+#pragma unroll 8
     for (int cc = 0; cc < nch; ++cc) {
-      if (cc == c) pre[tid] = tot;
-      tot += lc[cc * n + tid];
+      const int v = lc[cc * n + tid];
+      mine += cc < c ? v : 0;
+      tot += v;
     }
+    pre[tid] = mine;
   }
   const int nb = (tot + bm - 1) / bm;
   const int incl = block_incl_scan(nb, wsum);  // (its barriers order the LDS accesses around it)
@@ -362,11 +366,14 @@ __global__ __launch_bounds__(kAlignThreads) void align_place_kernel(const void* 
     sorted_ids[r] = (int32_t)S;
   if (c == 0 && tid == 0) npp[0] = used * bm;
   for (int e = tid; e < n; e += kAlignThreads) {        // offsets: earlier chunks, then earlier waves
+    int cw[kAlignWaves];
+#pragma unroll
+    for (int v = 0; v < kAlignWaves; ++v) cw[v] = wcnt[v][e];   // (all reads before the writes)
     int acc = pre[e];
+#pragma unroll
     for (int v = 0; v < kAlignWaves; ++v) {
-      const int cw = wcnt[v][e];
       wcnt[v][e] = acc;
-      acc += cw;
+      acc += cw[v];
     }
   }
   __syncthreads();
