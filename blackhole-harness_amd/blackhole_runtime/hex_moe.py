@@ -43,6 +43,8 @@ DIRECT_MAX = int(os.environ.get("BLACKHOLE_HEX_DIRECT_MAX", "32"))      # slots 
 # slots from which path="auto" takes the dequant path (hex_moe.py:261); never unless set
 DEQUANT_MIN = int(os.environ.get("BLACKHOLE_HEX_DEQUANT_MIN", str(1 << 62)))
 PREFILL_MIN = 40     # slots per expert above which the fused path takes the 128-slot prefill kernels
+PREFILL_MIN_LARGE = 35   # the same for expert matrices of 4M weights or more (config 5's 4096 x 1536)
+PREFILL_LARGE = 1 << 22
 DECODE16_MAX = 12    # slots per expert up to which the decode kernels take 16-slot blocks
 # a single tier's experts run as SPLIT parts on as many streams through the prefill kernels (see
 # hex_moe_fused); 1 or less keeps the tier whole. Two parts measured best: 433 / 439 / 447 us for
@@ -250,13 +252,17 @@ def default_config(slots: int, n_out: int, n_in: int, glu: bool, n_experts: int 
     their weights twice, and 32-slot blocks measured 352 against 434 us; at 10.7 (config 2,
     T=128) the two tie, and at 5.3 (T=64) 16-slot blocks win, 91 against 97 us. The 128-slot
     prefill kernels above 40 slots per expert: at 64 (config 5, T=1024) 728 against 890 us on
-    32-slot blocks, at 42.7 (config 2, T=512) a tie, at 32 (config 5, T=512) 690 against 550."""
+    32-slot blocks, at 42.7 (config 2, T=512) a tie, at 32 (config 5, T=512) 690 against 550. With
+    the 16-wave 4-bit prefill kernels the crossover fell for large experts (n_out x n_in of 4M or
+    more) and stayed for config 2's: config 5 at 34 slots per expert 569 (32-slot blocks) against
+    581 us, at 36 632 against 584, at 38 651 against 587; config 2 at 40 158 against 173 us."""
     env = os.environ.get("BLACKHOLE_HEX_TILES")
     if env:
         bm = _tile_from({"BLOCK_M": int(env.split(",")[0])})
     else:
         per_expert = slots / max(1, n_experts or slots)
-        bm = 16 if per_expert <= DECODE16_MAX else (32 if per_expert <= PREFILL_MIN else 128)
+        pmin = PREFILL_MIN_LARGE if n_out * n_in >= PREFILL_LARGE else PREFILL_MIN
+        bm = 16 if per_expert <= DECODE16_MAX else (32 if per_expert <= pmin else 128)
     return {"BLOCK_M": _fit_tile(bm, n_in, n_out, glu), "BLOCK_N": 256}
 
 

@@ -79,6 +79,10 @@ def test_default_config_and_env(monkeypatch):
     assert hm.default_config(3000, 768, 2048, True, 96)["BLOCK_M"] == 32                   # 31 per expert
     assert hm.default_config(96 * 40, 768, 2048, True, 96)["BLOCK_M"] == 32                # 40 per expert
     assert hm.default_config(96 * 41, 768, 2048, True, 96)["BLOCK_M"] == 128               # (64 never by default)
+    # experts of 4M weights or more (config 5) take the prefill kernels above 35 slots per expert
+    assert hm.default_config(128 * 35, 1536, 4096, True, 128)["BLOCK_M"] == 32
+    assert hm.default_config(128 * 36, 1536, 4096, True, 128)["BLOCK_M"] == 128
+    assert hm.default_config(128 * 36, 4096, 1536, False, 128)["BLOCK_M"] == 128
     monkeypatch.setenv("BLACKHOLE_HEX_TILES", "64")
     assert hm.default_config(8, 768, 2048, True, 96) == {"BLOCK_M": 64, "BLOCK_N": 256}
     # the reference's own config keys map onto the tile
