@@ -42,7 +42,7 @@ HEX_BLOCK = 32     # inputs per bit stream (blackhole/anatomy/hex.py:44)
 DIRECT_MAX = int(os.environ.get("BLACKHOLE_HEX_DIRECT_MAX", "32"))      # slots (hex_moe.py:260)
 # slots from which path="auto" takes the dequant path (hex_moe.py:261); never unless set
 DEQUANT_MIN = int(os.environ.get("BLACKHOLE_HEX_DEQUANT_MIN", str(1 << 62)))
-PREFILL_MIN = 40     # slots per expert above which the fused path takes the 128-slot prefill kernels
+PREFILL_MIN = 48     # slots per expert above which the fused path takes the 128-slot prefill kernels
 PREFILL_MIN_LARGE = 35   # the same for expert matrices of 4M weights or more (config 5's 4096 x 1536)
 PREFILL_LARGE = 1 << 22
 DECODE16_MAX = 12    # slots per expert up to which the decode kernels take 16-slot blocks
@@ -251,11 +251,11 @@ def default_config(slots: int, n_out: int, n_in: int, glu: bool, n_experts: int 
     expert on average: at 16 (config 5, T=256) the experts that get more than 16 slots stream
     their weights twice, and 32-slot blocks measured 352 against 434 us; at 10.7 (config 2,
     T=128) the two tie, and at 5.3 (T=64) 16-slot blocks win, 91 against 97 us. The 128-slot
-    prefill kernels above 40 slots per expert: at 64 (config 5, T=1024) 728 against 890 us on
-    32-slot blocks, at 42.7 (config 2, T=512) a tie, at 32 (config 5, T=512) 690 against 550. With
-    the 16-wave 4-bit prefill kernels the crossover fell for large experts (n_out x n_in of 4M or
-    more) and stayed for config 2's: config 5 at 34 slots per expert 569 (32-slot blocks) against
-    581 us, at 36 632 against 584, at 38 651 against 587; config 2 at 40 158 against 173 us."""
+    prefill kernels above PREFILL_MIN (48) slots per expert, or above PREFILL_MIN_LARGE (35) for
+    expert matrices of 4M weights or more (n_out x n_in), measured with the current kernels:
+    config 5 (4096 x 1536) at 34 slots per expert 569 us on 32-slot blocks against 581 us, at 36
+    632 against 584, at 38 651 against 587; config 2 (2048 x 768) at 40 158 against 173 us, at
+    42.7 162 against 172, at 53.3 178 against 176, at 64 187 against 180."""
     env = os.environ.get("BLACKHOLE_HEX_TILES")
     if env:
         bm = _tile_from({"BLOCK_M": int(env.split(",")[0])})

@@ -77,8 +77,8 @@ def test_default_config_and_env(monkeypatch):
     assert hm.default_config(32768, 2048, 768, False, 96)["BLOCK_M"] == 128                # prefill
     assert hm.default_config(32768, 2048, 96, False, 96)["BLOCK_M"] == 32                  # inputs % 128 != 0
     assert hm.default_config(3000, 768, 2048, True, 96)["BLOCK_M"] == 32                   # 31 per expert
-    assert hm.default_config(96 * 40, 768, 2048, True, 96)["BLOCK_M"] == 32                # 40 per expert
-    assert hm.default_config(96 * 41, 768, 2048, True, 96)["BLOCK_M"] == 128               # (64 never by default)
+    assert hm.default_config(96 * 48, 768, 2048, True, 96)["BLOCK_M"] == 32                # 48 per expert
+    assert hm.default_config(96 * 49, 768, 2048, True, 96)["BLOCK_M"] == 128               # (64 never by default)
     # experts of 4M weights or more (config 5) take the prefill kernels above 35 slots per expert
     assert hm.default_config(128 * 35, 1536, 4096, True, 128)["BLOCK_M"] == 32
     assert hm.default_config(128 * 36, 1536, 4096, True, 128)["BLOCK_M"] == 128
