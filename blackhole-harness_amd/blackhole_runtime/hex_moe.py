@@ -47,8 +47,8 @@ PREFILL_MIN_LARGE = 35   # the same for expert matrices of 4M weights or more (c
 PREFILL_LARGE = 1 << 22
 DECODE16_MAX = 12    # slots per expert up to which the decode kernels take 16-slot blocks
 # a single tier's experts run as SPLIT parts on as many streams through the prefill kernels (see
-# hex_moe_fused); 1 or less keeps the tier whole. Two parts measured best: 433 / 439 / 447 us for
-# 2 / 3 / 4 parts at config 3, 1116 / 1136 / 1155 us at config 5 (T=2048).
+# hex_moe_fused); 1 or less keeps the tier whole. Two parts measured best: 409 / 412 / 413 us for
+# 2 / 1 / 3 parts at config 3, 912 / 937 / 931 us at config 5 (T=2048; 16-wave 4-bit kernels).
 SPLIT = int(os.environ.get("BLACKHOLE_HEX_SPLIT", "2"))
 # slots up to which the decode kernels sort the slots by expert themselves (bh_hex_moe_*_ids), so
 # no align launch precedes them (at most 1024; 0 always launches the align kernel)
