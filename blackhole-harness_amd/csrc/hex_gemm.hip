@@ -8,9 +8,9 @@
 //
 //  * One workgroup per tile of 128 slots x R weight rows of one expert (R = 256 at 3 bits, 512 at
 //    4 bits; the workgroup's waves per GemmShape below): down takes R output rows; GLU takes R / 2
-//    outputs, i.e. the same rows of gate and of up. Each wave holds all 128 slots x 16 NG weight rows (NG groups of
-//    16; GLU: half gate, half the same up rows) in accumulator tiles, so every weight is decoded
-//    by exactly one wave.
+//    outputs, i.e. the same rows of gate and of up. Each wave holds all 128 slots x 16 NG weight
+//    rows (NG groups of 16; GLU: half gate, half the same up rows) in accumulator tiles, so every
+//    weight is decoded by exactly one wave.
 //  * The inputs run in steps of 128 (4 HEX blocks, 4 MFMA k-slices). A step's activation tile
 //    (128 gathered slot rows x 128 inputs, 32 KB) is loaded once per workgroup and staged
 //    through a two-stage LDS ring in the MFMA's fragment order, so every fragment read is one
@@ -85,6 +85,8 @@ __global__ __launch_bounds__((GemmShape<BITS, SB>::THREADS), (GemmShape<BITS, SB
   // copies keep down's reads conflict-free; GLU's gate and up tables get 16 copies each).
   constexpr int TC = BITS == 4 ? 64 : 32;
   constexpr int ES = TC == 64 ? 8 : 7;           // log2 of an entry's bytes
+  static_assert((NPAIR * TC / 4) % kGThreads == 0, "the table build gives every thread whole 16-byte stores");
+  static_assert(kGWaves * kChunks == 32 && 8 + kNG <= 16 && kChunks <= 8, "a step's loads fit its 16 m-tile slots");
   // Activation ring depth: tiles are loaded one step ahead of the math, as are the weight
   // words (two register sets). (Two steps ahead measured no faster.)
   constexpr int D = 2;
@@ -215,8 +217,8 @@ __global__ __launch_bounds__((GemmShape<BITS, SB>::THREADS), (GemmShape<BITS, SB
   // stays unconditional), then the math of this one:
   // per half step (two k-slices) the groups' operands from the table, then per m-tile j the two
   // activation fragments (those of j + 1 are read before the MFMAs of j) and per group a
-  // two-MFMA chain, whose block partial (128-input scales) is scaled into the accumulator one
-  // m-tile later (4-bit gate/up: at once); at 32-input scales each MFMA's partial is scaled.
+  // two-MFMA chain, whose block partial (128-input scales) is scaled into the accumulator; at
+  // 32-input scales each MFMA's partial is scaled.
   auto step = [&](int st, auto phase) {
     constexpr int P = decltype(phase)::value;
     const uint32_t* at = sm.atile[st % D];
@@ -311,6 +313,7 @@ __global__ __launch_bounds__((GemmShape<BITS, SB>::THREADS), (GemmShape<BITS, SB
     constexpr int RS = kCols + 8;                        // halves per staged row
     constexpr int PR = 32768 / RS >= kGM ? kGM : kGM / 2;
     constexpr int TPR = kCols / 8;                       // threads per row, 8 outputs (16 bytes) each
+    static_assert(PR * RS <= 32768 && (PR * TPR) % kGThreads == 0 && kGM % PR == 0, "GLU staging passes");
     uint16_t* const st16 = reinterpret_cast<uint16_t*>(stage);
 #pragma unroll
     for (int p = 0; p < kGM / PR; ++p) {
@@ -345,6 +348,7 @@ __global__ __launch_bounds__((GemmShape<BITS, SB>::THREADS), (GemmShape<BITS, SB
     // y in the activation dtype
     constexpr int PR = 32768 / kCols;                    // slot rows per pass
     constexpr int TPR = kCols / 8;
+    static_assert((PR * TPR) % kGThreads == 0 && kGM % PR == 0 && PR % 16 == 0, "16-bit y staging passes");
     uint16_t* const st16 = reinterpret_cast<uint16_t*>(stage);
 #pragma unroll
     for (int p = 0; p < kGM / PR; ++p) {
@@ -378,6 +382,7 @@ __global__ __launch_bounds__((GemmShape<BITS, SB>::THREADS), (GemmShape<BITS, SB
     // float32 y
     constexpr int PR = 16384 / kCols;                    // slot rows per pass
     constexpr int TPR = kCols / 4;                       // threads per row, 4 outputs (16 bytes) each
+    static_assert((PR * TPR) % kGThreads == 0 && kGM % PR == 0 && PR % 16 == 0, "float32 y staging passes");
     float* const stf = reinterpret_cast<float*>(stage);
 #pragma unroll
     for (int p = 0; p < kGM / PR; ++p) {
